@@ -1,0 +1,155 @@
+"""MI355X implementation of the FlashPrefill V1 stage functions.
+
+Same names, signatures, dtypes and layouts as the reference module
+``upstream/flashprefill_native_forward.py`` (all tensors ``[batch, sequence,
+heads, dim]``); each function enqueues hand-written gfx950 HIP kernels through
+the C ABI on the current stream. Tensors must be on a ROCm GPU.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+SCORE_IMPL = "v1_kmean_qt_row_reduce"
+LSE_IMPL = "natural_log_exact_lse"
+
+# Fixed launch geometry of the HIP kernels (the reference autotunes; these are
+# what its introspection helpers report here).
+ATTENTION_Q_TILE = 128   # query rows per workgroup
+ATTENTION_K_TILE = 128   # keys per LDS tile
+SCORE_K_TILE = 32        # key blocks per score MFMA chunk
+
+
+def _blocks(sequence: int, block_size: int) -> int:
+    return (sequence + block_size - 1) // block_size
+
+
+@torch.no_grad()
+def block_mean_k(k: torch.Tensor, block_size: int = 128) -> torch.Tensor:
+    """bf16 mean of K over each block's valid tokens, ``[B, NB, Hkv, D]``.
+
+    Reference: upstream/flashprefill_native_forward.py:420-442.
+    """
+    device = _lib.require_gpu(k)
+    k = _lib.kernel_view(k)
+    batch, sequence, kv_heads, head_dim = k.shape
+    mean = torch.empty(batch, _blocks(sequence, block_size), kv_heads, head_dim,
+                       dtype=k.dtype, device=device)
+    _lib.call("spx_block_mean_k", _lib.ptr(k), _lib.strides(k), batch, sequence, kv_heads,
+              head_dim, block_size, _lib.ptr(mean), _lib.stream(device))
+    return mean
+
+
+@torch.no_grad()
+def v1_scores(q: torch.Tensor, mean_k: torch.Tensor, scale: float,
+              block_size: int = 128) -> torch.Tensor:
+    """Normalised V1 block scores ``[B, NB, NB, Hq]`` (fp32).
+
+    Reference: upstream/flashprefill_native_forward.py:445-475 (the block score
+    kernel plus ``normalize_scores``, fused into one HIP kernel).
+    """
+    device = _lib.require_gpu(q, mean_k)
+    q = _lib.kernel_view(q)
+    mean_k = _lib.kernel_view(mean_k)
+    batch, sequence, q_heads, head_dim = q.shape
+    blocks = mean_k.shape[1]
+    if blocks != _blocks(sequence, block_size):
+        raise ValueError(f"mean_k has {blocks} blocks, expected {_blocks(sequence, block_size)}")
+    if mean_k.shape[0] != batch or mean_k.shape[3] != head_dim or q_heads % mean_k.shape[2]:
+        raise ValueError(f"mean_k shape {tuple(mean_k.shape)} does not match q {tuple(q.shape)}")
+    score = torch.empty(batch, blocks, blocks, q_heads, dtype=torch.float32, device=device)
+    _lib.call("spx_v1_scores", _lib.ptr(q), _lib.strides(q), _lib.ptr(mean_k),
+              _lib.strides(mean_k), batch, sequence, q_heads, mean_k.shape[2], head_dim,
+              block_size, float(scale), _lib.ptr(score), _lib.strides(score),
+              _lib.stream(device))
+    return score
+
+
+def deal_output_score(score: torch.Tensor, attention_sink: int, window: int,
+                      alpha: float = 0.1, last_n_blocks_full: int = 2, min_budget: int = 0):
+    """V1 threshold + protected selection -> (indices int64, counts int32).
+
+    Reference: upstream/flashprefill_native_forward.py:357-407. Outputs are fresh
+    tensors (no buffer reuse across calls).
+    """
+    device = _lib.require_gpu(score)
+    if score.dtype != torch.float32 or score.dim() != 4:
+        raise ValueError("score must be a float32 [batch, query_block, key_block, head] tensor")
+    batch, query_blocks, key_blocks, heads = score.shape
+    indices = torch.empty(batch, query_blocks, key_blocks, heads, dtype=torch.int64, device=device)
+    counts = torch.empty(batch, query_blocks, heads, dtype=torch.int32, device=device)
+    _lib.call("spx_deal_output_score", _lib.ptr(score), _lib.strides(score), batch,
+              query_blocks, key_blocks, heads, int(attention_sink), int(window), float(alpha),
+              int(last_n_blocks_full), int(min_budget), _lib.ptr(indices), _lib.ptr(counts),
+              None, _lib.stream(device))
+    return indices, counts
+
+
+def value_tiles(v: torch.Tensor, block_size: int = 128) -> torch.Tensor:
+    """Transposed, key-permuted per-block V tiles the attention kernel reads
+    (``[B, Hkv, NB, D, 128]`` bf16); produced by the pooling pass."""
+    device = _lib.require_gpu(v)
+    v = _lib.kernel_view(v)
+    batch, sequence, kv_heads, head_dim = v.shape
+    tiles = torch.empty(batch, kv_heads, _blocks(sequence, block_size), head_dim, block_size,
+                        dtype=torch.bfloat16, device=device)
+    _lib.call("spx_block_pool", None, None, _lib.ptr(v), _lib.strides(v), batch, sequence,
+              kv_heads, head_dim, block_size, None, None, None, None, None, None,
+              _lib.ptr(tiles), _lib.stream(device))
+    return tiles
+
+
+@torch.no_grad()
+def exact_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    indices: torch.Tensor, counts: torch.Tensor, scale: float,
+                    block_size: int = 128):
+    """Block-sparse causal attention -> (output bf16 ``[B,S,Hq,D]``, natural LSE fp32).
+
+    Reference: upstream/flashprefill_native_forward.py:478-521.
+    """
+    device = _lib.require_gpu(q, k, v, indices, counts)
+    q = _lib.kernel_view(q)
+    k = _lib.kernel_view(k)
+    if indices.dtype != torch.int64 or counts.dtype != torch.int32:
+        raise ValueError("indices must be int64 and counts int32")
+    batch, sequence, q_heads, head_dim = q.shape
+    check_attention_shapes(q, k, v, indices, counts, block_size)
+    tiles = value_tiles(v, block_size)
+    output = torch.empty(batch, sequence, q_heads, head_dim, dtype=q.dtype, device=device)
+    lse = torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
+    _lib.call("spx_exact_attention", _lib.ptr(q), _lib.strides(q), _lib.ptr(k), _lib.strides(k),
+              _lib.ptr(tiles), _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
+              _lib.strides(counts), batch, sequence, q_heads, k.shape[2], head_dim, block_size,
+              float(scale), _lib.ptr(output), _lib.strides(output), _lib.ptr(lse),
+              _lib.strides(lse), _lib.stream(device))
+    return output, lse
+
+
+def check_attention_shapes(q, k, v, indices, counts, block_size=128):
+    """Host-side shape validation: the kernels index these buffers by the
+    geometry derived from q."""
+    batch, sequence, q_heads, head_dim = q.shape
+    blocks = _blocks(sequence, block_size)
+    if k.dim() != 4 or k.shape[0] != batch or k.shape[1] != sequence or k.shape[3] != head_dim:
+        raise ValueError(f"k shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    if v is not None and tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"v shape {tuple(v.shape)} does not match k {tuple(k.shape)}")
+    if q_heads % k.shape[2]:
+        raise ValueError(f"q heads {q_heads} not a multiple of kv heads {k.shape[2]}")
+    if indices is not None and tuple(indices.shape) != (batch, blocks, blocks, q_heads):
+        raise ValueError(f"indices shape {tuple(indices.shape)}, expected "
+                         f"{(batch, blocks, blocks, q_heads)}")
+    if counts is not None and tuple(counts.shape) != (batch, blocks, q_heads):
+        raise ValueError(f"counts shape {tuple(counts.shape)}, expected {(batch, blocks, q_heads)}")
+
+
+def attention_tile_sizes():
+    """(query tile, key tile) of the attention kernel (upstream :524-528)."""
+    return ATTENTION_Q_TILE, ATTENTION_K_TILE
+
+
+def score_tile_size():
+    """Key blocks per score MFMA chunk (upstream :531-533)."""
+    return SCORE_K_TILE

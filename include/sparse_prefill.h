@@ -1,0 +1,217 @@
+/*
+ * C ABI of the MI355X (gfx950) sparse-prefill attention library
+ * (exp3_amd/_C/libexp3_amd.so).
+ *
+ * The reference (Yuhang-dev/exp3) has no native FFI: its hot path is Python
+ * functions over Triton kernels and PyTorch ops. Each entry point below replaces
+ * one of those Python functions and cites it (paths relative to the reference
+ * repository). The Python wrappers in exp3_amd/ keep the reference names,
+ * argument meanings, dtypes and exceptions and call these through ctypes.
+ *
+ * Conventions
+ *   - Device pointers only; every buffer is allocated by the caller. No entry
+ *     point allocates, frees or synchronises; work is enqueued on `stream`
+ *     (a hipStream_t, NULL = default stream).
+ *   - Tensors in the reference's [batch, sequence, heads, dim] order are passed
+ *     as a base pointer plus int64 strides in ELEMENTS (4 for [B,S,H,D], 3 for
+ *     [B,S,H]); the innermost (dim) stride must be 1.
+ *   - Score / mask / index tensors use [batch, query_block, key_block, head].
+ *     Outputs documented as "contiguous" must be densely packed in that order.
+ *   - bf16 tensors are raw 16-bit bf16 bit patterns; masks are uint8 (0 / 1).
+ *   - head_dim must be 128 and block_size 128 (the Qwen2.5-7B routing shape);
+ *     q_heads must be a multiple of kv_heads.
+ *   - Return 0 on success or a negative SPX_E* code; spx_last_error() then
+ *     returns a thread-local message.
+ */
+#ifndef EXP3_AMD_SPARSE_PREFILL_H
+#define EXP3_AMD_SPARSE_PREFILL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPX_OK 0
+#define SPX_EINVAL (-1)       /* bad argument: shape, stride, null pointer     */
+#define SPX_EUNSUPPORTED (-2) /* valid in the reference, not built here       */
+#define SPX_ELAUNCH (-3)      /* HIP launch / runtime failure                 */
+
+#define SPX_ABI_VERSION 1
+
+/* Selector ids for spx_selector_scores (kernels.py:62). */
+#define SPX_SELECTOR_MEAN_BALANCED 0
+#define SPX_SELECTOR_CGF_MEAN 1
+#define SPX_SELECTOR_DISPERSION_MEAN 2
+
+const char* spx_last_error(void);
+int spx_abi_version(void);
+
+/* ------------------------------------------------------------- pooling */
+
+/* bf16 block mean of K over the valid tokens of each 128-token block.
+ * Replaces upstream/flashprefill_native_forward.py:420-442 (block_mean_k) and its
+ * Triton kernel compute_mean_vector (:27-69).
+ * mean_k: contiguous [B, NB, Hkv, D] bf16, NB = ceil(seq / 128). */
+int spx_block_mean_k(const void* k, const int64_t* k_strides, int batch, int seq,
+                     int kv_heads, int head_dim, int block_size, void* mean_k,
+                     void* stream);
+
+/* FP32 block descriptors: mean_k, mean_v, var_k (contiguous [B, NB, Hkv, D]),
+ * sigma_v ([B, NB, Hkv]) and counts ([NB] int32).
+ * Replaces kernels.py:22-46 (block_descriptors). */
+int spx_block_descriptors(const void* k, const int64_t* k_strides, const void* v,
+                          const int64_t* v_strides, int batch, int seq, int kv_heads,
+                          int head_dim, int block_size, float* mean_k, float* mean_v,
+                          float* var_k, float* sigma_v, int32_t* counts, void* stream);
+
+/* One pass over K and V producing any subset of: bf16 mean K (as
+ * spx_block_mean_k), the FP32 descriptors (as spx_block_descriptors) and the
+ * value tiles the attention entry points read. Null outputs are skipped.
+ * value_tiles: [B, Hkv, NB, D, 128] bf16, V transposed per block with the key
+ * permutation documented in exp3_amd/csrc/common.h; keys past seq are zero.
+ * Fuses kernels.py:22-46 with upstream/flashprefill_native_forward.py:420-442
+ * (the descriptor stage of attention.py:80-86). */
+int spx_block_pool(const void* k, const int64_t* k_strides, const void* v,
+                   const int64_t* v_strides, int batch, int seq, int kv_heads,
+                   int head_dim, int block_size, void* mean_k_bf16, float* mean_k,
+                   float* mean_v, float* var_k, float* sigma_v, int32_t* counts,
+                   void* value_tiles, void* stream);
+
+/* ------------------------------------------------------------- routing */
+
+/* Normalised V1 block scores, written to score (strided [B, NB, NB, Hq] fp32;
+ * every entry is written, entries with key block > query block are 0).
+ * Replaces upstream/flashprefill_native_forward.py:445-475 (v1_scores), i.e. the
+ * Triton kernel compute_block_score (:89-175) followed by normalize_scores
+ * (:410-417). mean_k is bf16 [B, NB, Hkv, D] with the given strides. */
+int spx_v1_scores(const void* q, const int64_t* q_strides, const void* mean_k,
+                  const int64_t* mean_k_strides, int batch, int seq, int q_heads,
+                  int kv_heads, int head_dim, int block_size, float scale,
+                  float* score, const int64_t* score_strides, void* stream);
+
+/* V1 threshold + protected selection with ascending index lists.
+ * keep = score >= fp32(max_j score * alpha) (or the min_budget branch), protected
+ * = j < attention_sink | 0 <= t - j < window | t >= query_blocks - last_n_blocks_full,
+ * active = (keep | protected) & j <= t.
+ * indices: contiguous [B, QB, KB, H] int64 (active ids ascending, then KB);
+ * counts: contiguous [B, QB, H] int32; mask: optional contiguous uint8 mask of the
+ * active set (what kernels.py:163-176 mask_from_indices would give).
+ * Replaces upstream/flashprefill_native_forward.py:357-407 (deal_output_score). */
+int spx_deal_output_score(const float* score, const int64_t* score_strides, int batch,
+                          int query_blocks, int key_blocks, int heads, int attention_sink,
+                          int window, float alpha, int last_n_blocks_full, int min_budget,
+                          int64_t* indices, int32_t* counts, uint8_t* mask, void* stream);
+
+/* Threshold selection of the new selectors: alpha == 0 selects every causal block,
+ * else routed = score > 0 & score >= fp32(alpha * max_j score), united with the
+ * protected set and intersected with j <= t. mask: contiguous uint8 [B,QB,KB,H];
+ * indices / counts optional (as spx_deal_output_score; kernels.py:154-160).
+ * Replaces kernels.py:129-151 (protected_selection). */
+int spx_protected_selection(const float* score, const int64_t* score_strides, int batch,
+                            int query_blocks, int key_blocks, int heads, float alpha,
+                            int sink_blocks, int window_blocks, int last_full_blocks,
+                            uint8_t* mask, int64_t* indices, int32_t* counts, void* stream);
+
+/* Fused V1 route: spx_v1_scores and spx_deal_output_score in one launch, the
+ * selection reading the exact score values it writes. score may be NULL (not
+ * stored); mask may be NULL. Replaces attention.py:87-105 (_v1_selection's
+ * selector + indices stages). */
+int spx_v1_route(const void* q, const int64_t* q_strides, const void* mean_k,
+                 const int64_t* mean_k_strides, int batch, int seq, int q_heads,
+                 int kv_heads, int head_dim, int block_size, float scale, float alpha,
+                 int attention_sink, int window, int last_n_blocks_full, float* score,
+                 int64_t* indices, int32_t* counts, uint8_t* mask, void* stream);
+
+/* kernels.py:154-160 (indices_from_mask). mask: contiguous uint8 [B,QB,KB,H]. */
+int spx_indices_from_mask(const uint8_t* mask, int batch, int query_blocks, int key_blocks,
+                          int heads, int64_t* indices, int32_t* counts, void* stream);
+
+/* kernels.py:163-176 (mask_from_indices). indices contiguous int64, counts int32. */
+int spx_mask_from_indices(const int64_t* indices, const int32_t* counts, int batch,
+                          int query_blocks, int key_blocks, int heads, uint8_t* mask,
+                          void* stream);
+
+/* Balanced / CGF / dispersion block scores (selector = SPX_SELECTOR_*), written to
+ * score (strided [B, NB, NB, Hq] fp32, every entry written).
+ * mean_k, var_k: contiguous fp32 [B, NB, Hkv, D]; sigma_v [B, NB, Hkv];
+ * counts [NB] int32. Replaces kernels.py:49-126 (selector_scores). */
+int spx_selector_scores(const void* q, const int64_t* q_strides, const float* mean_k,
+                        const float* var_k, const float* sigma_v, const int32_t* counts,
+                        int batch, int seq, int q_heads, int kv_heads, int head_dim,
+                        int block_size, int selector, float scale, float* score,
+                        const int64_t* score_strides, void* stream);
+
+/* ----------------------------------------------------------- attention */
+
+/* Block-sparse causal flash attention over each (query tile, head)'s index list.
+ * value_tiles come from spx_block_pool. indices: int64 [B, NB, NB, Hq] (strided),
+ * counts: int32 [B, NB, Hq] (strided); indices == NULL selects every causal block
+ * (dense causal attention). out: bf16 [B, S, Hq, D] (strided); lse: natural-log LSE
+ * fp32 [B, S, Hq] (strided, may be NULL).
+ * Replaces upstream/flashprefill_native_forward.py:478-521 (exact_attention) and the
+ * Triton kernel _flash_forward (:215-354). */
+int spx_exact_attention(const void* q, const int64_t* q_strides, const void* k,
+                        const int64_t* k_strides, const void* value_tiles,
+                        const int64_t* indices, const int64_t* index_strides,
+                        const int32_t* counts, const int64_t* count_strides, int batch,
+                        int seq, int q_heads, int kv_heads, int head_dim, int block_size,
+                        float scale, void* out, const int64_t* out_strides, float* lse,
+                        const int64_t* lse_strides, void* stream);
+
+/* Exact attention with the block-mean correction fused in: each row additionally
+ * attends to the fp32 mean K / mean V (logit + ln n_j) of every full-history block
+ * j < t that is not in its tile's list, inside the same online softmax, so the
+ * result equals the logaddexp merge of the exact and mean paths.
+ * mean_k, mean_v: contiguous fp32 [B, NB, Hkv, D]; block_counts: [NB] int32.
+ * Replaces the exact + mean + merge stages of attention.py:253-305:
+ * upstream exact_attention, kernels.py:179-230 (mean_tail) and kernels.py:312-325
+ * (merge_exact_mean). */
+int spx_sparse_attention_mean(const void* q, const int64_t* q_strides, const void* k,
+                              const int64_t* k_strides, const void* value_tiles,
+                              const int64_t* indices, const int64_t* index_strides,
+                              const int32_t* counts, const int64_t* count_strides,
+                              const float* mean_k, const float* mean_v,
+                              const int32_t* block_counts, int batch, int seq, int q_heads,
+                              int kv_heads, int head_dim, int block_size, float scale,
+                              void* out, const int64_t* out_strides, float* lse,
+                              const int64_t* lse_strides, void* stream);
+
+/* Mean path alone: fp32 output and LSE of each row against the mean K / V of the
+ * unselected full-history blocks of its tile (selection given as index lists,
+ * e.g. from spx_indices_from_mask). out: fp32 [B, S, Hq, D] strided; lse strided.
+ * Replaces kernels.py:179-230 (mean_tail). */
+int spx_mean_tail(const void* q, const int64_t* q_strides, const int64_t* indices,
+                  const int64_t* index_strides, const int32_t* counts,
+                  const int64_t* count_strides, const float* mean_k, const float* mean_v,
+                  const int32_t* block_counts, int batch, int seq, int q_heads, int kv_heads,
+                  int head_dim, int block_size, float scale, float* out,
+                  const int64_t* out_strides, float* lse, const int64_t* lse_strides,
+                  void* stream);
+
+/* logaddexp merge of an exact (bf16 output, fp32 LSE) and a mean (fp32 output,
+ * fp32 LSE) path; writes bf16 output and fp32 total LSE (lse_out may be NULL).
+ * Replaces kernels.py:312-325 (merge_exact_mean). */
+int spx_merge_exact_mean(const void* exact_out, const int64_t* exact_strides,
+                         const float* exact_lse, const int64_t* exact_lse_strides,
+                         const float* mean_out, const int64_t* mean_strides,
+                         const float* mean_lse, const int64_t* mean_lse_strides, int batch,
+                         int seq, int heads, int head_dim, void* out,
+                         const int64_t* out_strides, float* lse_out,
+                         const int64_t* lse_out_strides, void* stream);
+
+/* ----------------------------------------------------------- accounting */
+
+/* Integer counters of kernels.py:328-407 (selection_accounting) from a contiguous
+ * uint8 mask [B, NB, NB, H]: totals[0] = exact token pairs, [1] = selected block
+ * entries, [2] = mean proxy entries, [3] = sum over selected entries of
+ * ceil(rows / q_tile) (times ceil(128 / k_tile) gives the physical QK tiles;
+ * q_tile <= 0 skips it). totals: 4 int64, overwritten. */
+int spx_selection_accounting(const uint8_t* mask, int batch, int blocks, int heads, int seq,
+                             int block_size, int q_tile, int64_t* totals, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXP3_AMD_SPARSE_PREFILL_H */

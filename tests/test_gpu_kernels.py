@@ -1,0 +1,251 @@
+"""Stage-level parity of the HIP kernels against the CPU oracle (check_math-style).
+
+Each test drives one C-ABI entry point through the reference-named Python
+wrapper on the same seeded inputs as the oracle. Bars: bit-exact for selection /
+index / mask work; the reference's own check_math tolerances (and the
+north-star max-abs 2e-2 / mean-abs 2e-3) for floating point.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from exp3_amd import kernels
+from exp3_amd.upstream import flashprefill_native_forward as up
+from oracle import reference_cpu as ref
+from tests.helpers import (SCALE, assert_output_close, inputs, masks_equal_except_ties,
+                           threshold_ties, to_np)
+
+pytestmark = pytest.mark.gpu
+
+LENGTHS = (257, 385, 1089)
+
+
+def _gpu(*ts):
+    return [t.to("cuda") for t in ts]
+
+
+@pytest.mark.parametrize("length", (257, 1089, 4096))
+def test_block_mean_k(gpu, length):
+    q, k, v = inputs(length)
+    kg, = _gpu(k)
+    actual = to_np(up.block_mean_k(kg))
+    expected = ref.block_mean_k(to_np(k))
+    # bf16 outputs: equal, or one bf16 ulp apart where the fp32 sum order decides rounding
+    ulp = np.abs(expected) * 2.0 ** -7 + 1e-30
+    diff = np.abs(actual - expected)
+    assert (diff <= ulp).all(), float((diff / ulp).max())
+    assert (diff == 0).mean() > 0.999
+    # check_math.py:292-300 tolerance against the plain fp32 mean
+    plain = np.stack([to_np(k)[:, s:s + 128].mean(axis=1) for s in range(0, length, 128)], axis=1)
+    np.testing.assert_allclose(actual, plain, atol=0.002, rtol=0.02)
+
+
+@pytest.mark.parametrize("length", LENGTHS)
+def test_block_descriptors(gpu, length):
+    q, k, v = inputs(length, seed=3)
+    kg, vg = _gpu(k, v)
+    d = kernels.block_descriptors(kg, vg)
+    e = ref.block_descriptors(to_np(k), to_np(v))
+    for name in ("mean_k", "mean_v", "var_k", "sigma_v"):
+        np.testing.assert_allclose(to_np(getattr(d, name)), getattr(e, name), atol=2e-6, rtol=2e-5,
+                                   err_msg=name)
+    np.testing.assert_array_equal(to_np(d.counts), e.counts)
+
+
+@pytest.mark.parametrize("length", (257, 1089))
+def test_value_tiles_layout(gpu, length):
+    q, k, v = inputs(length, seed=5)
+    vg, = _gpu(v)
+    tiles = to_np(up.value_tiles(vg))          # [B, Hkv, NB, D, 128]
+    vv = to_np(v)
+    blocks = tiles.shape[2]
+    for slot in range(128):
+        c16, s = divmod(slot, 16)
+        key = c16 * 16 + 4 * (s // 8) + (s % 4) + 8 * ((s % 8) // 4)
+        for j in range(blocks):
+            token = j * 128 + key
+            want = vv[:, token].transpose(0, 1, 2) if token < length else np.zeros_like(vv[:, 0])
+            np.testing.assert_array_equal(tiles[:, :, j, :, slot], want)
+
+
+@pytest.mark.parametrize("length", (257, 1089, 4096))
+def test_v1_scores(gpu, length):
+    q, k, v = inputs(length, seed=11)
+    qg, kg = _gpu(q, k)
+    kbar = up.block_mean_k(kg)
+    actual = to_np(up.v1_scores(qg, kbar, SCALE))
+    expected = ref.v1_scores(to_np(q), to_np(kbar), SCALE)
+    np.testing.assert_allclose(actual, expected, atol=2e-4, rtol=0.005)   # check_math.py:301-303
+    rows = actual.sum(axis=2)
+    assert np.all(np.isclose(rows, 1.0, atol=1e-5) | np.isclose(rows, 0.0, atol=1e-9))
+    upper = np.triu(np.ones((actual.shape[1],) * 2, dtype=bool), k=1)
+    assert (actual[:, upper] == 0).all()
+
+
+def _adversarial_scores(length, seed):
+    """Score tensors that stress the threshold: raised-to-the-4th V1 scores
+    (check_math.py:305-311), exact ties with the threshold, zero rows."""
+    q, k, v = inputs(length, seed=seed)
+    kbar = ref.block_mean_k(to_np(k))
+    s = ref.v1_scores(to_np(q), kbar, SCALE)
+    s4 = (s * s) * (s * s)
+    tied = s.copy()
+    tied[:, :, 0, :] = 1.0
+    tied[:, :, 1, :] = np.float32(np.float32(1.0) * np.float32(0.08))   # exactly at threshold
+    tied[:, :, 2, :] = np.nextafter(tied[:, :, 1, :], np.float32(0))     # one ulp below
+    zero = np.zeros_like(s)
+    return [(s4.astype(np.float32), 0.8), (s, 0.08), (tied.astype(np.float32), 0.08),
+            (zero, 0.08), (s, 0.0)]
+
+
+@pytest.mark.parametrize("length", (385, 1089))
+def test_deal_output_score_bit_exact(gpu, length):
+    for scores, alpha in _adversarial_scores(length, seed=23):
+        sg = torch.from_numpy(scores).cuda()
+        for sink, window, last in ((2, 4, 2), (1, 1, 0), (0, 0, 3)):
+            idx, cnt = up.deal_output_score(sg, sink, window, alpha, last, 0)
+            e_idx, e_cnt = ref.deal_output_score(scores, sink, window, alpha, last, 0)
+            np.testing.assert_array_equal(to_np(idx), e_idx)
+            np.testing.assert_array_equal(to_np(cnt), e_cnt)
+
+
+def test_deal_output_score_min_budget(gpu):
+    scores, _ = _adversarial_scores(1089, seed=29)[0]
+    sg = torch.from_numpy(scores).cuda()
+    idx, cnt = up.deal_output_score(sg, 2, 4, 0.9, 2, 3)
+    e_idx, e_cnt = ref.deal_output_score(scores, 2, 4, 0.9, 2, 3)
+    np.testing.assert_array_equal(to_np(idx), e_idx)
+    np.testing.assert_array_equal(to_np(cnt), e_cnt)
+
+
+@pytest.mark.parametrize("length", (385, 1089))
+def test_protected_selection_bit_exact(gpu, length):
+    for scores, alpha in _adversarial_scores(length, seed=31):
+        sg = torch.from_numpy(scores).cuda()
+        mask = kernels.protected_selection(sg, alpha, 2, 4, 2)
+        expected = ref.protected_selection(scores, alpha, 2, 4, 2)
+        np.testing.assert_array_equal(to_np(mask), expected)
+        idx, cnt = kernels.indices_from_mask(mask)
+        e_idx, e_cnt = ref.indices_from_mask(expected)
+        np.testing.assert_array_equal(to_np(idx), e_idx)
+        np.testing.assert_array_equal(to_np(cnt), e_cnt)
+        back = kernels.mask_from_indices(idx, cnt)
+        np.testing.assert_array_equal(to_np(back), expected)
+
+
+@pytest.mark.parametrize("length", (257, 1089))
+@pytest.mark.parametrize("selector", ("mean_balanced", "cgf_mean", "dispersion_mean"))
+def test_selector_scores(gpu, length, selector):
+    q, k, v = inputs(length, seed=41)
+    qg, kg, vg = _gpu(q, k, v)
+    desc = kernels.block_descriptors(kg, vg)
+    actual = to_np(kernels.selector_scores(qg, desc, SCALE, selector))
+    e_desc = ref.BlockDescriptors(*(to_np(getattr(desc, n)) for n in
+                                    ("mean_k", "mean_v", "var_k", "sigma_v", "counts")))
+    expected = ref.selector_scores(to_np(q), e_desc, SCALE, selector)
+    np.testing.assert_allclose(actual, expected, atol=2e-5, rtol=2e-5)   # check_math.py:287-290
+
+
+def _fixed_selection(length, seed, drop=0.3):
+    """All-causal selection with a random share of full-history blocks removed
+    (protected blocks kept), as in check_math.py:245-250."""
+    blocks = ref.num_blocks(length)
+    rng = np.random.default_rng(seed)
+    sel = ref.protected_selection(np.zeros((1, blocks, blocks, 28), np.float32), 0.0, 2, 4, 2)
+    drop_mask = rng.random(sel.shape) < drop
+    t = np.arange(blocks).reshape(1, -1, 1, 1)
+    j = np.arange(blocks).reshape(1, 1, -1, 1)
+    droppable = (j < t) & (j >= 1)
+    sel = sel & ~(drop_mask & droppable)
+    return sel
+
+
+@pytest.mark.parametrize("length", (257, 1089))
+def test_exact_attention_all_selected_vs_dense(gpu, length):
+    q, k, v = inputs(length, seed=17)
+    qg, kg, vg = _gpu(q, k, v)
+    blocks = ref.num_blocks(length)
+    sel = np.broadcast_to(np.tril(np.ones((blocks, blocks), bool))[None, :, :, None],
+                          (1, blocks, blocks, 28))
+    idx, cnt = ref.indices_from_mask(sel)
+    out, lse = up.exact_attention(qg, kg, vg, torch.from_numpy(idx).cuda(),
+                                  torch.from_numpy(cnt).cuda(), SCALE)
+    d_out, d_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE)
+    assert_output_close(to_np(out), d_out)
+    np.testing.assert_allclose(to_np(lse), d_lse, atol=0.02, rtol=0.01)   # check_math.py:243
+
+
+@pytest.mark.parametrize("length", (385, 1089, 4096))
+def test_exact_attention_fixed_mask(gpu, length):
+    q, k, v = inputs(length, seed=19)
+    qg, kg, vg = _gpu(q, k, v)
+    sel = _fixed_selection(length, seed=7)
+    idx, cnt = ref.indices_from_mask(sel)
+    out, lse = up.exact_attention(qg, kg, vg, torch.from_numpy(idx).cuda(),
+                                  torch.from_numpy(cnt).cuda(), SCALE)
+    e_out, e_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE)
+    assert_output_close(to_np(out), e_out)
+    np.testing.assert_allclose(to_np(lse), e_lse, atol=0.02, rtol=0.01)
+
+
+def test_exact_attention_edge_lists(gpu):
+    """Empty list -> output 0 / LSE -inf; a list holding only a future block and
+    an out-of-range id follows the kernel's documented semantics."""
+    length = 385
+    q, k, v = inputs(length, seed=2)
+    qg, kg, vg = _gpu(q, k, v)
+    blocks = ref.num_blocks(length)
+    idx = np.full((1, blocks, blocks, 28), blocks, np.int64)
+    cnt = np.zeros((1, blocks, 28), np.int32)
+    idx[0, 1, 0, 3] = 2      # future block for tile 1, head 3
+    cnt[0, 1, 3] = 1
+    idx[0, 2, 0, 5] = 2      # diagonal + an out-of-range id
+    idx[0, 2, 1, 5] = 99
+    cnt[0, 2, 5] = 2
+    out, lse = up.exact_attention(qg, kg, vg, torch.from_numpy(idx).cuda(),
+                                  torch.from_numpy(cnt).cuda(), SCALE)
+    e_out, e_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE)
+    a_out, a_lse = to_np(out), to_np(lse)
+    assert_output_close(a_out, e_out)
+    finite = np.isfinite(e_lse)
+    np.testing.assert_array_equal(np.isfinite(a_lse), finite)
+    np.testing.assert_allclose(a_lse[finite], e_lse[finite], atol=0.02, rtol=0.01)
+    assert (a_out[~finite] == 0).all()
+
+
+@pytest.mark.parametrize("length", (257, 1089))
+def test_mean_tail_and_merge(gpu, length):
+    q, k, v = inputs(length, seed=37)
+    qg, kg, vg = _gpu(q, k, v)
+    sel = _fixed_selection(length, seed=9, drop=0.5)
+    desc = kernels.block_descriptors(kg, vg)
+    e_desc = ref.block_descriptors(to_np(k), to_np(v))
+    sg = torch.from_numpy(sel).cuda()
+    m_out, m_lse = kernels.mean_tail(qg, desc, sg, SCALE)
+    e_out, e_lse = ref.mean_tail(to_np(q), e_desc, sel, SCALE)
+    np.testing.assert_allclose(to_np(m_out), e_out, atol=2e-3, rtol=2e-2)
+    finite = np.isfinite(e_lse)
+    np.testing.assert_array_equal(np.isfinite(to_np(m_lse)), finite)
+    np.testing.assert_allclose(to_np(m_lse)[finite], e_lse[finite], atol=2e-3, rtol=1e-3)
+    idx, cnt = ref.indices_from_mask(sel)
+    x_out, x_lse = up.exact_attention(qg, kg, vg, torch.from_numpy(idx).cuda(),
+                                      torch.from_numpy(cnt).cuda(), SCALE)
+    merged, total = kernels.merge_exact_mean(x_out, x_lse, m_out, m_lse)
+    r_out, r_total = ref.merge_exact_mean(to_np(x_out), to_np(x_lse), to_np(m_out), to_np(m_lse))
+    assert_output_close(to_np(merged), r_out, max_abs=8e-3, mean_abs=1e-4, what="merge")
+    np.testing.assert_allclose(to_np(total), r_total, atol=1e-5, rtol=1e-5)
+
+
+def test_selection_accounting(gpu):
+    sel = _fixed_selection(1089, seed=4)
+    acct = kernels.selection_accounting(torch.from_numpy(sel).cuda(), 1089, 128, 128,
+                                        "mean_native", 32)
+    expected = ref.selection_accounting(sel, 1089, 128, 128, "mean_native", 32)
+    for key, value in expected.items():
+        got = acct[key]
+        got = got.item() if isinstance(got, torch.Tensor) else got
+        if isinstance(value, float):
+            assert got == pytest.approx(value, rel=1e-12), key
+        else:
+            assert got == value, key
