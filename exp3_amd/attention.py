@@ -87,6 +87,9 @@ class AttentionBackend:
         self.record = False
         self.profile_records = []
         self.capture_callback = None
+        # When a list, every attention-kernel launch appends its (start, end)
+        # torch.cuda.Event pair, recorded on the launch stream (benchmarks).
+        self.kernel_events = None
         if register and ALL_ATTENTION_FUNCTIONS is not None:
             ALL_ATTENTION_FUNCTIONS["sdpa"] = self.forward
 
@@ -207,11 +210,18 @@ class AttentionBackend:
         common_tail = (batch, sequence, q_heads, k.shape[2], head_dim, self.block_size,
                        float(scale), _lib.ptr(output), _lib.strides(output), _lib.ptr(lse),
                        _lib.strides(lse), _lib.stream(device))
+        events = None
+        if self.kernel_events is not None:
+            events = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            events[0].record()
         if descriptors is None:
             _lib.call("spx_exact_attention", *common_head, *common_tail)
         else:
             _lib.call("spx_sparse_attention_mean", *common_head, _lib.ptr(descriptors.mean_k),
                       _lib.ptr(descriptors.mean_v), _lib.ptr(descriptors.counts), *common_tail)
+        if events is not None:
+            events[1].record()
+            self.kernel_events.append(events)
         return output, lse
 
     def _dense_hip(self, q, k, v, scale):

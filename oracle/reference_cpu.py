@@ -378,36 +378,51 @@ def exact_attention(q, k, v, indices, counts, scale, block_size: int = BLOCK_SIZ
     blocks = num_blocks(sequence, block_size)
     kp = _pad_blocks(k, block_size)
     vp = _pad_blocks(v, block_size)
-    group = q_heads // k.shape[2]
+    kv_heads = k.shape[2]
+    group = q_heads // kv_heads
     out = np.zeros(q.shape, dtype=np.float32)
     lse = np.full((batch, sequence, q_heads), -np.inf, dtype=np.float32)
-    tile_ids = range(num_blocks(sequence, block_size)) if tiles is None else tiles
+    tile_ids = range(blocks) if tiles is None else tiles
     with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
         for b in range(batch):
             for t in tile_ids:
                 row0, row1 = t * block_size, min(sequence, (t + 1) * block_size)
+                rows = row1 - row0
                 query_pos = np.arange(row0, row1)
-                for h in range(q_heads):
-                    count = int(counts[b, t, h])
-                    listed = [int(j) for j in indices[b, t, :max(count, 0), h]]
-                    listed = [j for j in listed if 0 <= j < blocks]
-                    if not listed:
-                        continue
-                    g = h // group
-                    keys = np.concatenate([kp[b, j, :, g] for j in listed]).astype(acc)
-                    values = np.concatenate([vp[b, j, :, g] for j in listed]).astype(acc)
-                    key_pos = np.concatenate(
-                        [np.arange(j * block_size, (j + 1) * block_size) for j in listed])
-                    on_diagonal = np.concatenate(
-                        [np.full(block_size, j == t) for j in listed])
-                    logits = q[b, row0:row1, h].astype(acc) @ keys.T * acc(scale)
-                    masked = on_diagonal[None, :] & (key_pos[None, :] > query_pos[:, None])
-                    logits = np.where(masked, -np.inf, logits)
-                    row_max = logits.max(axis=1, keepdims=True)
-                    weights = np.exp(logits - row_max)
-                    total = weights.sum(axis=1, keepdims=True)
-                    out[b, row0:row1, h] = ((weights @ values) / total).astype(np.float32)
-                    lse[b, row0:row1, h] = (row_max[:, 0] + np.log(total[:, 0])).astype(np.float32)
+                for g in range(kv_heads):
+                    # heads of the group that share one list are evaluated together
+                    by_list = {}
+                    for h in range(g * group, (g + 1) * group):
+                        count = max(int(counts[b, t, h]), 0)
+                        listed = tuple(int(j) for j in indices[b, t, :count, h]
+                                       if 0 <= int(j) < blocks)
+                        by_list.setdefault(listed, []).append(h)
+                    for listed, heads in by_list.items():
+                        if not listed:
+                            continue
+                        keys = kp[b, list(listed), :, g].reshape(-1, dim).astype(acc)
+                        values = vp[b, list(listed), :, g].reshape(-1, dim).astype(acc)
+                        key_pos = (np.asarray(listed)[:, None] * block_size
+                                   + np.arange(block_size)[None, :]).reshape(-1)
+                        diag_cols = np.nonzero(np.repeat(np.asarray(listed) == t, block_size))[0]
+                        query = q[b, row0:row1][:, heads].transpose(1, 0, 2).reshape(-1, dim)
+                        logits = query.astype(acc) @ keys.T
+                        logits *= acc(scale)
+                        logits = logits.reshape(len(heads), rows, -1)
+                        if diag_cols.size:
+                            masked = key_pos[diag_cols][None, :] > query_pos[:, None]
+                            sub = logits[:, :, diag_cols]
+                            sub[:, masked] = -np.inf
+                            logits[:, :, diag_cols] = sub
+                        row_max = logits.max(axis=2, keepdims=True)
+                        logits -= row_max
+                        weights = np.exp(logits, out=logits)
+                        total = weights.sum(axis=2, keepdims=True)
+                        result = (weights.reshape(-1, weights.shape[2]) @ values).reshape(
+                            len(heads), rows, dim) / total
+                        out[b, row0:row1][:, heads] = result.transpose(1, 0, 2).astype(np.float32)
+                        lse[b, row0:row1][:, heads] = (row_max[..., 0] + np.log(total[..., 0])
+                                                       ).T.astype(np.float32)
     return bf16_round(out), lse
 
 
