@@ -18,7 +18,7 @@ SPX_OK = 0
 SPX_EINVAL = -1
 SPX_EUNSUPPORTED = -2
 SPX_ELAUNCH = -3
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 SELECTOR_IDS = {"mean_balanced": 0, "cgf_mean": 1, "dispersion_mean": 2}
 
@@ -31,7 +31,7 @@ _S = ctypes.POINTER(ctypes.c_int64)
 _PROTOTYPES = {
     "spx_block_mean_k": [_P, _S, _I, _I, _I, _I, _I, _P, _P],
     "spx_block_descriptors": [_P, _S, _P, _S, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
-    "spx_block_pool": [_P, _S, _P, _S, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P],
+    "spx_block_pool": [_P, _S, _P, _S, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "spx_v1_scores": [_P, _S, _P, _S, _I, _I, _I, _I, _I, _I, _F, _P, _S, _P],
     "spx_deal_output_score": [_P, _S, _I, _I, _I, _I, _I, _I, _F, _I, _I, _P, _P, _P, _P],
     "spx_protected_selection": [_P, _S, _I, _I, _I, _I, _F, _I, _I, _I, _P, _P, _P, _P],
@@ -40,9 +40,9 @@ _PROTOTYPES = {
     "spx_indices_from_mask": [_P, _I, _I, _I, _I, _P, _P, _P],
     "spx_mask_from_indices": [_P, _P, _I, _I, _I, _I, _P, _P],
     "spx_selector_scores": [_P, _S, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _S, _P],
-    "spx_exact_attention": [_P, _S, _P, _S, _P, _P, _S, _P, _S, _I, _I, _I, _I, _I, _I, _F, _P,
+    "spx_exact_attention": [_P, _S, _P, _P, _P, _S, _P, _S, _I, _I, _I, _I, _I, _I, _F, _P,
                             _S, _P, _S, _P],
-    "spx_sparse_attention_mean": [_P, _S, _P, _S, _P, _P, _S, _P, _S, _P, _P, _P, _I, _I, _I, _I,
+    "spx_sparse_attention_mean": [_P, _S, _P, _P, _P, _S, _P, _S, _P, _P, _P, _I, _I, _I, _I,
                                   _I, _I, _F, _P, _S, _P, _S, _P],
     "spx_mean_tail": [_P, _S, _P, _S, _P, _S, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _S, _P,
                       _S, _P],

@@ -6,7 +6,7 @@ names, profiling and capture hooks, and the same registration as transformers'
 ``"sdpa"`` attention function (attention.py:57). Prefill of the sparse methods
 runs entirely in gfx950 HIP kernels:
 
-  descriptor  spx_block_pool           bf16 mean K, fp32 descriptors, value tiles
+  descriptor  spx_block_pool           bf16 mean K, fp32 descriptors, K / V tiles
   selector    spx_v1_route             V1 score + normalise + threshold selection
               spx_selector_scores      (mean_balanced / cgf_mean / dispersion_mean)
   indices     spx_protected_selection  (new selectors; V1 selection is fused above)
@@ -114,7 +114,8 @@ class AttentionBackend:
     # ------------------------------------------------------------ pooling
 
     def _pool(self, k, v, want_kbar: bool, want_descriptors: bool, want_tiles: bool):
-        """One spx_block_pool launch -> (bf16 mean K, descriptors, value tiles)."""
+        """One spx_block_pool launch -> (bf16 mean K, descriptors, (key tiles,
+        value tiles))."""
         device = _lib.require_gpu(k, v)
         batch, sequence, kv_heads, head_dim = k.shape
         blocks = _blocks(sequence, self.block_size)
@@ -122,14 +123,17 @@ class AttentionBackend:
                            device=device) if want_kbar else None
         desc = kernels.empty_descriptors(batch, blocks, kv_heads, head_dim, device) \
             if want_descriptors else None
-        tiles = torch.empty(batch, kv_heads, blocks, head_dim, self.block_size,
-                            dtype=torch.bfloat16, device=device) if want_tiles else None
+        tiles = (torch.empty(batch, kv_heads, blocks, self.block_size, head_dim,
+                             dtype=torch.bfloat16, device=device),
+                 torch.empty(batch, kv_heads, blocks, head_dim, self.block_size,
+                             dtype=torch.bfloat16, device=device)) if want_tiles else None
         _lib.call(
             "spx_block_pool", _lib.ptr(k), _lib.strides(k), _lib.ptr(v), _lib.strides(v),
             batch, sequence, kv_heads, head_dim, self.block_size, _lib.ptr(kbar),
             _lib.ptr(desc.mean_k if desc else None), _lib.ptr(desc.mean_v if desc else None),
             _lib.ptr(desc.var_k if desc else None), _lib.ptr(desc.sigma_v if desc else None),
-            _lib.ptr(desc.counts if desc else None), _lib.ptr(tiles), _lib.stream(device))
+            _lib.ptr(desc.counts if desc else None), _lib.ptr(tiles[0] if tiles else None),
+            _lib.ptr(tiles[1] if tiles else None), _lib.stream(device))
         return kbar, desc, tiles
 
     # ---------------------------------------------------------- selection
@@ -175,7 +179,7 @@ class AttentionBackend:
         return descriptors, indices, counts, selected
 
     def _new_selection(self, q, k, v, scale, record, want_tiles=False):
-        """Reference attention.py:110-152 (plus the value tiles of the pooling pass)."""
+        """Reference attention.py:110-152 (plus the attention tiles of the pooling pass)."""
         _, descriptors, tiles = self._stage(
             record, "descriptor", lambda: self._pool(k, v, False, True, want_tiles))
         batch, sequence, q_heads, _ = q.shape
@@ -204,7 +208,7 @@ class AttentionBackend:
         batch, sequence, q_heads, head_dim = q.shape
         output = torch.empty(batch, sequence, q_heads, head_dim, dtype=q.dtype, device=device)
         lse = torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
-        common_head = (_lib.ptr(q), _lib.strides(q), _lib.ptr(k), _lib.strides(k), _lib.ptr(tiles),
+        common_head = (_lib.ptr(q), _lib.strides(q), _lib.ptr(tiles[0]), _lib.ptr(tiles[1]),
                        _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
                        _lib.strides(counts))
         common_tail = (batch, sequence, q_heads, k.shape[2], head_dim, self.block_size,

@@ -6,39 +6,45 @@
 // index list in order; every listed 128-key block j contributes all its keys
 // (keys past the sequence end read as zero), causality is applied only inside the
 // block j == t; O = softmax(scale q K^T) V is stored as bf16 and the natural-log
-// LSE = M ln 2 + ln l. With the mean correction, each row also attends to the fp32
-// block-mean key of every block j < t missing from its list (logit + ln n_j) with
-// the block-mean value, inside the same online softmax; this equals the logaddexp
-// merge of kernels.py:179-230 (mean_tail) and :312-325 (merge_exact_mean).
+// LSE = M ln 2 + ln l. List entries outside [0, NB) are skipped. With the mean
+// correction, each row also attends to the fp32 block-mean key of every block
+// j < t missing from its list (logit + ln n_j) with the block-mean value, inside
+// the same online softmax; this equals the logaddexp merge of kernels.py:179-230
+// (mean_tail) and :312-325 (merge_exact_mean).
 //
 // gfx950 design
-//   * One workgroup (4 waves) per (query tile, q head); wave w owns query rows
-//     32w .. 32w + 31 of the tile and keeps them in registers as the B operand.
+//   * One workgroup (4 waves, 32 query rows each) per (query tile, q head); two
+//     workgroups per CU (66 KB LDS each), so one's tile loads and barriers overlap
+//     the other's math.
 //   * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16:
-//     each lane owns ONE query column, so the row max / row sum are in-lane
-//     reductions plus a single exchange with the other lane half, the O rescale is
-//     a per-lane scalar, and the probabilities already sit in the B-operand layout
-//     of O^T = V^T P^T: no shuffles and no LDS round trip for P.
-//   * K (row-major) and the pre-transposed value tile (from the pooling pass) are
-//     staged through LDS with 16-byte accesses; 16-byte chunks are XOR-swizzled by
-//     row so the MFMA operand reads are bank-conflict free.
-//   * Grid order: (tile, kv group) pairs heaviest-first, and the heads of one
-//     group are consecutive on the same XCD (workgroup i runs on XCD i % 8), so the
-//     seven q heads sharing a KV block read it from the same L2.
+//     each lane owns one query column, so row max / row sum are in-lane reductions
+//     plus one exchange with the other lane half, the O rescale is a per-lane
+//     scalar, and the probabilities already sit in the B-operand layout of
+//     O^T = V^T P^T (no shuffles, no LDS round trip for P).
+//   * K rows and the pre-transposed value tile come from the pooling pass already
+//     in LDS order (XOR-swizzled 16-byte chunks, conflict-free operand reads) and
+//     are copied with direct global->LDS loads (no staging registers). Operand
+//     reads are issued one MFMA step ahead.
+//   * Full blocks run without masks; on the diagonal block wave w touches only key
+//     sub-blocks 0 .. w. The running max moves lazily (only by more than 2^8), so
+//     the O rescale is a rarely taken wave-uniform branch.
+//   * Grid order: (tile, kv group) pairs heaviest-first, and the heads of one group
+//     consecutive on the same XCD (workgroup i runs on XCD i % 8), so the seven q
+//     heads sharing a KV block read it from the same L2.
 #include "common.h"
 
 namespace spx {
 
-constexpr int kAttnThreads = 256;
+constexpr int kAttnThreads = 256;     // 4 waves x 32 query rows
 constexpr int kMaxBlocksAttn = 1024;
-constexpr int kTailTile = 64;  // mean keys per tail tile (hi and lo halves fill K LDS)
+constexpr int kTailTile = 64;        // mean keys per tail tile (hi and lo rows fill K LDS)
+constexpr float kLazyRescale = 8.0f; // log2 headroom before a column's running max moves
 
 struct AttnArgs {
   const uint16_t* q;
   int64_t qs_b, qs_s, qs_h;
-  const uint16_t* k;
-  int64_t ks_b, ks_s, ks_h;
-  const uint16_t* vt;  // [B, Hkv, NB, D, 128]
+  const uint16_t* kt;  // key tiles   [B, Hkv, NB, 128, D]  (LDS order, from the pool pass)
+  const uint16_t* vt;  // value tiles [B, Hkv, NB, D, 128]
   const int64_t* idx;  // nullable: all causal blocks
   int64_t is_b, is_t, is_p, is_h;
   const int32_t* cnt;
@@ -71,68 +77,186 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& v, int base) {
   return as_bf16x8(w);
 }
 
-// One key tile of the online softmax. s[mb] holds raw q.k dots for key sub-block mb
-// (keys 32 mb + mfma32_row(r, lane)) of this lane's query column; only the first
-// `nmb` sub-blocks exist. `diag` applies key > query masking inside the tile;
-// `bias` (LDS, per key, base-2 units, may be null) is added after scaling.
-__device__ __forceinline__ void online_tile(f32x16 (&s)[4], int nmb, bool diag, int qpos,
-                                            const float* bias, float scale_log2,
-                                            const uint16_t* v_lds, float& m_run,
-                                            float& l_run, f32x16 (&o)[4]) {
+// Per-wave online-softmax state for its 32 query columns.
+struct WaveState {
+  bf16x8 qb[8];   // Q^T B operands, dim chunk dc
+  f32x16 o[4];    // O^T accumulators, dim block db
+  float m;        // running max (base-2, scaled), lazily moved
+  float l;        // running sum over this lane half's keys
+};
+
+// Copy one 32 KB tile, already in LDS order in global memory, into LDS with
+// direct global->LDS loads: lane l of a wave lands at (wave base) + 16 l, so
+// thread id moves 16-byte chunks id + 256 i. No VGPRs are used for staging;
+// completion is awaited with wait_tiles() before the publishing barrier.
+__device__ __forceinline__ void dma_tile(const uint16_t* src, uint16_t* lds, int tid) {
+  const int w = tid >> 6, lane = tid & 63;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int chunk0 = i * kAttnThreads + w * 64;
+    const uint16_t* g = src + (int64_t)(chunk0 + lane) * 8;
+    uint16_t* l = lds + chunk0 * 8;
+    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
+                                     (void __attribute__((address_space(3)))*)l, 16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void wait_tiles() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// LDS element offset of this lane's MFMA operand row (row & 15 == col & 15 for
+// every operand row it reads) with 16-byte chunk 2 x + half, for x = 0: the chunk
+// for any other x is base ^ (x << 4) (XOR swizzle c ^ (row & 15), c = 2 x + half).
+__device__ __forceinline__ int operand_base(int row) {
   const int lane = threadIdx.x & 63;
   const int col = lane & 31, half = lane >> 5;
+  const int cx = (col >> 1) & 7, hb = half ^ (col & 1);
+  return row * kBlock + (cx << 4) + (hb << 3);
+}
+
+// Keep `x` opaque inside a loop so derived addresses are recomputed per use
+// instead of being hoisted (and held) as a table of loop invariants.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Compiler fence: nothing is scheduled across it. Keeps operand reads issued a
+// step ahead of the MFMAs that consume them.
+__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// S^T for NMB 32-key sub-blocks at K rows row0 + 32 mb + col (for hi/lo mean
+// keys, also rows + kTailTile). The NMB (x2) operand reads of a dim chunk are
+// issued one chunk ahead of their MFMAs.
+template <int NMB, bool HILO>
+__device__ __forceinline__ void scores(const uint16_t* kb, const WaveState& ws, int row0,
+                                       f32x16 (&s)[4]) {
+  constexpr int P = NMB * (HILO ? 2 : 1);
+  const int col = threadIdx.x & 31;
+  const int e0 = opaque(operand_base(row0 + col));
+  auto row_off = [](int part) {
+    return HILO ? ((part & 1) ? kTailTile * kBlock : 0) + (part >> 1) * 32 * kBlock
+                : part * 32 * kBlock;
+  };
+  bf16x8 ring[2][P];
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) s[mb] = f32x16{};
+#pragma unroll
+  for (int p = 0; p < P; ++p) ring[0][p] = lds_read16(kb, e0 + row_off(p));
+  fence();
+#pragma unroll
+  for (int dc = 0; dc < 8; ++dc) {
+    if (dc + 1 < 8) {
+      const int e = e0 ^ ((dc + 1) << 4);
+#pragma unroll
+      for (int p = 0; p < P; ++p) ring[(dc + 1) & 1][p] = lds_read16(kb, e + row_off(p));
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int mb = HILO ? (p >> 1) : p;
+      s[mb] = mfma32(ring[dc & 1][p], ws.qb[dc], s[mb]);
+    }
+    fence();
+  }
+}
+
+// Softmax of one tile: masks (DIAG) / per-key biases (BIAS, already scaled),
+// lazily moved running max, probabilities packed to bf16 B operands pb[2 mb + h],
+// running sum, O rescale when any lane moved its max.
+template <int NMB, bool DIAG, bool BIAS>
+__device__ __forceinline__ void softmax(f32x16 (&s)[4], WaveState& ws, float scale, int q_pos,
+                                        const float* bias, int bias_row0, bf16x8 (&pb)[8]) {
+  const int lane = threadIdx.x & 63;
   float mx = -INFINITY;
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    if (mb < nmb) {
+  for (int mb = 0; mb < NMB; ++mb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = mb * 32 + mfma32_row(r, lane);
-        float x = s[mb][r] * scale_log2;
-        if (bias) x += bias[key];
-        if (diag && key > qpos) x = -INFINITY;
-        s[mb][r] = x;
-        mx = fmaxf(mx, x);
-      }
+    for (int r = 0; r < 16; ++r) {
+      float x = s[mb][r];
+      if (BIAS) x = fmaf(x, scale, bias[bias_row0 + mb * 32 + mfma32_row(r, lane)]);
+      if (DIAG && mb * 32 + mfma32_row(r, lane) > q_pos) x = -INFINITY;
+      s[mb][r] = x;
+      mx = fmaxf(mx, x);
     }
   }
   mx = fmaxf(mx, xor32(mx));
-  const float m_new = fmaxf(m_run, mx);
-  const float corr = (m_run == m_new) ? 1.0f : exp2_fast(m_run - m_new);
-  const float msub = (m_new == -INFINITY) ? 0.0f : m_new;
-  float rowsum = 0.0f;
+  const float mxs = BIAS ? mx : mx * scale;
+  const float m_new = (mxs > ws.m + kLazyRescale) ? mxs : ws.m;
+  if (__any(m_new != ws.m)) {
+    const float corr = (m_new == ws.m) ? 1.0f : exp2_fast(ws.m - m_new);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) ws.o[db] *= corr;
+    ws.l *= corr;
+    ws.m = m_new;
+  }
+  const float neg_m = (ws.m == -INFINITY) ? 0.0f : -ws.m;
+  float sum = 0.0f;
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = BIAS ? exp2_fast(s[mb][r] + neg_m) : exp2_fast(fmaf(s[mb][r], scale, neg_m));
+      s[mb][r] = p;
+      sum += p;
+    }
+    pb[2 * mb] = pack8(s[mb], 0);
+    pb[2 * mb + 1] = pack8(s[mb], 8);
+  }
+  ws.l += sum;
+}
+
+// O^T += V^T P^T over NKC 16-key chunks (value chunks 0 .. NKC-1); the four
+// value-tile reads of a chunk are issued one chunk ahead.
+template <int NKC>
+__device__ __forceinline__ void accumulate_pv(const uint16_t* vb, WaveState& ws,
+                                              const bf16x8 (&pb)[8]) {
+  const int col = threadIdx.x & 31;
+  const int e0 = opaque(operand_base(col));
+  bf16x8 ring[2][4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) ring[0][db] = lds_read16(vb, e0 + db * 32 * kBlock);
+  fence();
+#pragma unroll
+  for (int kc = 0; kc < NKC; ++kc) {
+    if (kc + 1 < NKC) {
+      const int e = e0 ^ ((kc + 1) << 4);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) ring[(kc + 1) & 1][db] = lds_read16(vb, e + db * 32 * kBlock);
+    }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) ws.o[db] = mfma32(ring[kc & 1][db], pb[kc], ws.o[db]);
+    fence();
+  }
+}
+
+// One exact block: full tiles use every key sub-block with no masking; on the
+// diagonal wave w only reaches sub-blocks 0 .. w (keys above its queries are
+// masked, sub-blocks beyond w are skipped entirely).
+template <int NMB, bool DIAG>
+__device__ __forceinline__ void exact_block(const uint16_t* kb, const uint16_t* vb, WaveState& ws,
+                                            float scale, int q_pos) {
+  f32x16 s[4];
   bf16x8 pb[8];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    if (mb < nmb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = exp2_fast(s[mb][r] - msub);
-        s[mb][r] = p;
-        rowsum += p;
-      }
-      pb[2 * mb] = pack8(s[mb], 0);
-      pb[2 * mb + 1] = pack8(s[mb], 8);
-    }
-  }
-  l_run = l_run * corr + rowsum;
-  m_run = m_new;
-  if (corr != 1.0f) {
-#pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] *= corr;
-  }
-  // O^T[d][q] += V^T[d][slot] P^T[slot][q]; slot chunk kc covers keys 16 kc .. 16 kc + 15.
-#pragma unroll
-  for (int kc = 0; kc < 8; ++kc) {
-    if (kc < 2 * nmb) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const bf16x8 va = lds_read16(v_lds, swz(db * 32 + col, kc * 2 + half));
-        o[db] = mfma32(va, pb[kc], o[db]);
-      }
-    }
-  }
-  (void)col;
+  scores<NMB, false>(kb, ws, 0, s);
+  softmax<NMB, DIAG, false>(s, ws, scale, q_pos, nullptr, 0, pb);
+  accumulate_pv<2 * NMB>(vb, ws, pb);
+}
+
+// Ascending compaction of flagged ids into LDS `list`; returns the count (all threads).
+__device__ __forceinline__ int compact_append(bool flag, int id, int16_t* list, int base,
+                                             int* wave_counts) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int nwaves = kAttnThreads / 64;
+  const uint64_t ballot = __ballot(flag);
+  const int before = __popcll(ballot & ((1ull << lane) - 1ull));
+  if (lane == 0) wave_counts[w] = __popcll(ballot);
+  __syncthreads();
+  int offset = base;
+  for (int x = 0; x < w; ++x) offset += wave_counts[x];
+  if (flag) list[offset + before] = (int16_t)id;
+  int total = base;
+  for (int x = 0; x < nwaves; ++x) total += wave_counts[x];
+  __syncthreads();
+  return total;
 }
 
 template <bool EXACT, bool TAIL, bool OUT_F32>
@@ -151,124 +275,102 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_kernel(AttnArgs a) {
   const int g = (pair % bg) % a.kv_heads;
   const int h = g * a.group + hg;
 
-  __shared__ __align__(16) uint16_t k_lds[kBlock * kBlock];
-  __shared__ __align__(16) uint16_t v_lds[kBlock * kBlock];
+  __shared__ __align__(16) uint16_t kbuf[kBlock * kBlock];
+  __shared__ __align__(16) uint16_t vbuf[kBlock * kBlock];
+  __shared__ int16_t blist[kMaxBlocksAttn];
+  __shared__ uint32_t listed[kMaxBlocksAttn / 32];
+  __shared__ float tail_bias[kTailTile];
+  __shared__ int wave_counts[kAttnThreads / 64];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
-  const int qpos = w * 32 + col;  // query position inside the tile
-  const int64_t qrow = (int64_t)t * kBlock + qpos;
+  const int q_pos = w * 32 + col;  // this lane's query inside the tile
+  const float scale = a.scale_log2;
 
-  bf16x8 qb[8];
+  WaveState ws;
   {
+    const int64_t qrow = (int64_t)t * kBlock + q_pos;
     const uint16_t* src = a.q + b * a.qs_b + qrow * a.qs_s + h * a.qs_h + half * 8;
     const bool ok = qrow < a.seq;
 #pragma unroll
     for (int dc = 0; dc < 8; ++dc) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (ok) raw = *reinterpret_cast<const u32x4*>(src + dc * 16);
-      qb[dc] = as_bf16x8(raw);
+      ws.qb[dc] = as_bf16x8(raw);
     }
-  }
-
-  float m_run = -INFINITY, l_run = 0.0f;
-  f32x16 o[4];
+    ws.m = -INFINITY;
+    ws.l = 0.0f;
 #pragma unroll
-  for (int db = 0; db < 4; ++db) o[db] = f32x16{};
-
-  int count;
-  if (a.idx) {
-    count = a.cnt[b * a.cs_b + t * a.cs_t + h * a.cs_h];
-    count = min(max(count, 0), a.blocks);
-  } else {
-    count = t + 1;
+    for (int db = 0; db < 4; ++db) ws.o[db] = f32x16{};
   }
-  const int64_t* list = a.idx ? a.idx + b * a.is_b + t * a.is_t + h * a.is_h : nullptr;
+
+  // ---- the tile's block list (valid ids, in list order) in LDS
+  int n = 0;
+  if (a.idx) {
+    int count = a.cnt[b * a.cs_b + t * a.cs_t + h * a.cs_h];
+    count = min(max(count, 0), a.blocks);
+    const int64_t* list = a.idx + b * a.is_b + t * a.is_t + h * a.is_h;
+    for (int p0 = 0; p0 < count; p0 += kAttnThreads) {
+      const int pos = p0 + tid;
+      int j = -1;
+      if (pos < count) j = (int)list[pos * a.is_p];
+      n = compact_append(pos < count && j >= 0 && j < a.blocks, j, blist, n, wave_counts);
+    }
+  } else {
+    n = t + 1;
+    for (int j = tid; j <= t; j += kAttnThreads) blist[j] = (int16_t)j;
+    __syncthreads();
+  }
+  n = __builtin_amdgcn_readfirstlane(n);
 
   if (EXACT) {
-    const uint16_t* kbase = a.k + b * a.ks_b + g * a.ks_h;
-    const uint16_t* vbase = a.vt + (((int64_t)b * a.kv_heads + g) * a.blocks) * (kHeadDim * kBlock);
-    for (int pos = 0; pos < count; ++pos) {
-      const int j = list ? (int)list[pos * a.is_p] : pos;
-      if (j < 0 || j >= a.blocks) continue;
-      // ---- stage K block j and its value tile into LDS
-      u32x4 kr[8], vr[8];
-      const uint16_t* vtile = vbase + (int64_t)j * (kHeadDim * kBlock);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int id = tid + kAttnThreads * i;
-        const int r = id >> 4, c = id & 15;
-        const int64_t tok = (int64_t)j * kBlock + r;
-        kr[i] = u32x4{0u, 0u, 0u, 0u};
-        if (tok < a.seq) kr[i] = *reinterpret_cast<const u32x4*>(kbase + tok * a.ks_s + c * 8);
-        vr[i] = *reinterpret_cast<const u32x4*>(vtile + r * kBlock + c * 8);
-      }
-      __syncthreads();  // previous tile fully consumed
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int id = tid + kAttnThreads * i;
-        const int r = id >> 4, c = id & 15;
-        *reinterpret_cast<u32x4*>(k_lds + swz(r, c)) = kr[i];
-        *reinterpret_cast<u32x4*>(v_lds + swz(r, c)) = vr[i];
-      }
+    const int64_t tile_elems = (int64_t)kBlock * kHeadDim;
+    const uint16_t* kbase = a.kt + (((int64_t)b * a.kv_heads + g) * a.blocks) * tile_elems;
+    const uint16_t* vbase = a.vt + (((int64_t)b * a.kv_heads + g) * a.blocks) * tile_elems;
+    for (int i = 0; i < n; ++i) {
+      const int j = __builtin_amdgcn_readfirstlane(blist[i]);
+      dma_tile(kbase + j * tile_elems, kbuf, tid);
+      dma_tile(vbase + j * tile_elems, vbuf, tid);
+      wait_tiles();
       __syncthreads();
-
-      const bool diag = j == t;
-      const int nmb = diag ? (w + 1) : 4;
-      f32x16 s[4];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) s[mb] = f32x16{};
-#pragma unroll
-      for (int dc = 0; dc < 8; ++dc) {
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          if (mb < nmb) {
-            const bf16x8 ka = lds_read16(k_lds, swz(mb * 32 + col, dc * 2 + half));
-            s[mb] = mfma32(ka, qb[dc], s[mb]);
-          }
+      if (j != t) {
+        exact_block<4, false>(kbuf, vbuf, ws, scale, q_pos);
+      } else {
+        switch (w) {  // wave w reaches key sub-blocks 0 .. w of the diagonal block
+          case 0: exact_block<1, true>(kbuf, vbuf, ws, scale, q_pos); break;
+          case 1: exact_block<2, true>(kbuf, vbuf, ws, scale, q_pos); break;
+          case 2: exact_block<3, true>(kbuf, vbuf, ws, scale, q_pos); break;
+          default: exact_block<4, true>(kbuf, vbuf, ws, scale, q_pos); break;
         }
       }
-      online_tile(s, nmb, diag, qpos, nullptr, a.scale_log2, v_lds, m_run, l_run, o);
+      __syncthreads();  // every wave is done with the tile before it is refilled
     }
   }
 
   if (TAIL) {
-    __shared__ uint32_t listed[kMaxBlocksAttn / 32];
-    __shared__ int16_t tail_ids[kMaxBlocksAttn];
-    __shared__ float tail_bias[kTailTile];
-    __shared__ int wave_counts[4];
-    __syncthreads();
+    // bitmap of listed blocks, then {j < t : not listed} ascending into blist
     if (tid < kMaxBlocksAttn / 32) listed[tid] = 0u;
     __syncthreads();
-    for (int pos = tid; pos < count; pos += kAttnThreads) {
-      const int j = list ? (int)list[pos * a.is_p] : pos;
-      if (j >= 0 && j < a.blocks) atomicOr(&listed[j >> 5], 1u << (j & 31));
+    for (int i = tid; i < n; i += kAttnThreads) {
+      const int j = blist[i];
+      atomicOr(&listed[j >> 5], 1u << (j & 31));
     }
     __syncthreads();
-    // ascending compaction of {j < t : j not listed}
     int ntail = 0;
     for (int j0 = 0; j0 < t; j0 += kAttnThreads) {
       const int j = j0 + tid;
       const bool in_tail = j < t && ((listed[j >> 5] >> (j & 31)) & 1u) == 0u;
-      const uint64_t ballot = __ballot(in_tail);
-      const int before = __popcll(ballot & ((1ull << lane) - 1ull));
-      if (lane == 0) wave_counts[w] = __popcll(ballot);
-      __syncthreads();
-      int offset = ntail;
-      for (int x = 0; x < w; ++x) offset += wave_counts[x];
-      if (in_tail) tail_ids[offset + before] = (int16_t)j;
-      for (int x = 0; x < 4; ++x) ntail += wave_counts[x];
-      __syncthreads();
+      ntail = compact_append(in_tail, j, blist, ntail, wave_counts);
     }
-
-    const int64_t desc_base = (int64_t)b * a.blocks * a.kv_heads + g;  // (b, 0, g) row
+    const int64_t desc_base = (int64_t)b * a.blocks * a.kv_heads + g;  // (b, 0, g)
     for (int t0 = 0; t0 < ntail; t0 += kTailTile) {
       __syncthreads();
-      // stage: K rows i (hi) and 64 + i (lo) of mean K; value slots 0..63 of mean V
+      // K rows i (hi) and 64 + i (lo) of mean K; value slots 0..63 of mean V
       for (int e = tid; e < kTailTile * kHeadDim; e += kAttnThreads) {
         const int i = e >> 7, d = e & 127;
-        const int j = (t0 + i < ntail) ? (int)tail_ids[t0 + i] : -1;
+        const int j = (t0 + i < ntail) ? (int)blist[t0 + i] : -1;
         float mk = 0.0f, mv = 0.0f;
         if (j >= 0) {
           const int64_t off = (desc_base + (int64_t)j * a.kv_heads) * kHeadDim + d;
@@ -277,35 +379,26 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_kernel(AttnArgs a) {
         }
         const uint16_t hi = to_bf16_bits(mk);
         const uint16_t lo = to_bf16_bits(mk - __uint_as_float((uint32_t)hi << 16));
-        k_lds[swz(i, d >> 3) + (d & 7)] = hi;
-        k_lds[swz(kTailTile + i, d >> 3) + (d & 7)] = lo;
+        kbuf[swz(i, d >> 3) + (d & 7)] = hi;
+        kbuf[swz(kTailTile + i, d >> 3) + (d & 7)] = lo;
         const int slot = value_slot_of_key(i);
-        v_lds[swz(d, slot >> 3) + (slot & 7)] = to_bf16_bits(mv);
-        if (d == 0)
-          tail_bias[i] = j >= 0 ? __logf((float)a.bcounts[j]) * kLog2e : -INFINITY;
+        vbuf[swz(d, slot >> 3) + (slot & 7)] = to_bf16_bits(mv);
+        if (d == 0) tail_bias[i] = j >= 0 ? logf((float)a.bcounts[j]) * kLog2e : -INFINITY;
       }
       __syncthreads();
       f32x16 s[4];
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) s[mb] = f32x16{};
-#pragma unroll
-      for (int dc = 0; dc < 8; ++dc) {
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-          const bf16x8 khi = lds_read16(k_lds, swz(mb * 32 + col, dc * 2 + half));
-          const bf16x8 klo = lds_read16(k_lds, swz(kTailTile + mb * 32 + col, dc * 2 + half));
-          s[mb] = mfma32(khi, qb[dc], s[mb]);
-          s[mb] = mfma32(klo, qb[dc], s[mb]);
-        }
-      }
-      online_tile(s, 2, false, qpos, tail_bias, a.scale_log2, v_lds, m_run, l_run, o);
+      bf16x8 pb[8];
+      scores<2, true>(kbuf, ws, 0, s);
+      softmax<2, false, true>(s, ws, scale, q_pos, tail_bias, 0, pb);
+      accumulate_pv<4>(vbuf, ws, pb);
     }
   }
 
   // ---- epilogue
-  const float l = l_run + xor32(l_run);
+  const float l = ws.l + xor32(ws.l);
   const bool any = l > 0.0f;
   const float inv = any ? 1.0f / l : 0.0f;
+  const int64_t qrow = (int64_t)t * kBlock + q_pos;
   if (qrow < a.seq) {
     if (OUT_F32) {
       float* dst = static_cast<float*>(a.out) + b * a.os_b + qrow * a.os_s + h * a.os_h;
@@ -314,9 +407,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int d0 = db * 32 + 8 * rr + 4 * half;
-          f32x4 v4 = {o[db][4 * rr] * inv, o[db][4 * rr + 1] * inv, o[db][4 * rr + 2] * inv,
-                      o[db][4 * rr + 3] * inv};
-          *reinterpret_cast<f32x4*>(dst + d0) = v4;
+          *reinterpret_cast<f32x4*>(dst + d0) =
+              f32x4{ws.o[db][4 * rr] * inv, ws.o[db][4 * rr + 1] * inv, ws.o[db][4 * rr + 2] * inv,
+                    ws.o[db][4 * rr + 3] * inv};
         }
       }
     } else {
@@ -327,14 +420,14 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_kernel(AttnArgs a) {
         for (int rr = 0; rr < 4; ++rr) {
           const int d0 = db * 32 + 8 * rr + 4 * half;
           u32x2 v2;
-          v2[0] = pack_bf16x2(o[db][4 * rr] * inv, o[db][4 * rr + 1] * inv);
-          v2[1] = pack_bf16x2(o[db][4 * rr + 2] * inv, o[db][4 * rr + 3] * inv);
+          v2[0] = pack_bf16x2(ws.o[db][4 * rr] * inv, ws.o[db][4 * rr + 1] * inv);
+          v2[1] = pack_bf16x2(ws.o[db][4 * rr + 2] * inv, ws.o[db][4 * rr + 3] * inv);
           *reinterpret_cast<u32x2*>(dst + d0) = v2;
         }
       }
     }
     if (a.lse && half == 0)
-      a.lse[b * a.ls_b + qrow * a.ls_s + h * a.ls_h] = any ? m_run * kLn2 + __logf(l) : -INFINITY;
+      a.lse[b * a.ls_b + qrow * a.ls_s + h * a.ls_h] = any ? ws.m * kLn2 + logf(l) : -INFINITY;
   }
 }
 
@@ -407,7 +500,7 @@ struct AttnRequest {
 };
 
 int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_strides,
-                     const void* k, const int64_t* k_strides, const void* value_tiles,
+                     const void* key_tiles, const void* value_tiles,
                      const int64_t* indices, const int64_t* index_strides,
                      const int32_t* counts, const int64_t* count_strides,
                      const float* mean_k, const float* mean_v, const int32_t* block_counts,
@@ -427,8 +520,8 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
   e = check_bsdh("out", out, out_strides, true);
   if (e) return e;
   if (req.exact) {
-    e = check_bsdh("k", k, k_strides, true);
-    if (e) return e;
+    SPX_REQUIRE(key_tiles != nullptr && (reinterpret_cast<uintptr_t>(key_tiles) & 15) == 0,
+                SPX_EINVAL, "key_tiles: null or not 16-byte aligned");
     SPX_REQUIRE(value_tiles != nullptr && (reinterpret_cast<uintptr_t>(value_tiles) & 15) == 0,
                 SPX_EINVAL, "value_tiles: null or not 16-byte aligned");
   }
@@ -447,8 +540,7 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
   AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.qs_b = q_strides[0]; a.qs_s = q_strides[1]; a.qs_h = q_strides[2];
-  a.k = static_cast<const uint16_t*>(k);
-  if (req.exact) { a.ks_b = k_strides[0]; a.ks_s = k_strides[1]; a.ks_h = k_strides[2]; }
+  a.kt = static_cast<const uint16_t*>(key_tiles);
   a.vt = static_cast<const uint16_t*>(value_tiles);
   a.idx = indices;
   if (indices) {
@@ -476,22 +568,22 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
 
 }  // namespace
 
-extern "C" int spx_exact_attention(const void* q, const int64_t* q_strides, const void* k,
-                                   const int64_t* k_strides, const void* value_tiles,
+extern "C" int spx_exact_attention(const void* q, const int64_t* q_strides,
+                                   const void* key_tiles, const void* value_tiles,
                                    const int64_t* indices, const int64_t* index_strides,
                                    const int32_t* counts, const int64_t* count_strides, int batch,
                                    int seq, int q_heads, int kv_heads, int head_dim,
                                    int block_size, float scale, void* out,
                                    const int64_t* out_strides, float* lse,
                                    const int64_t* lse_strides, void* stream) {
-  return launch_attention({true, false, false}, q, q_strides, k, k_strides, value_tiles, indices,
+  return launch_attention({true, false, false}, q, q_strides, key_tiles, value_tiles, indices,
                           index_strides, counts, count_strides, nullptr, nullptr, nullptr, batch,
                           seq, q_heads, kv_heads, head_dim, block_size, scale, out, out_strides,
                           lse, lse_strides, stream);
 }
 
-extern "C" int spx_sparse_attention_mean(const void* q, const int64_t* q_strides, const void* k,
-                                         const int64_t* k_strides, const void* value_tiles,
+extern "C" int spx_sparse_attention_mean(const void* q, const int64_t* q_strides,
+                                         const void* key_tiles, const void* value_tiles,
                                          const int64_t* indices, const int64_t* index_strides,
                                          const int32_t* counts, const int64_t* count_strides,
                                          const float* mean_k, const float* mean_v,
@@ -499,7 +591,7 @@ extern "C" int spx_sparse_attention_mean(const void* q, const int64_t* q_strides
                                          int q_heads, int kv_heads, int head_dim, int block_size,
                                          float scale, void* out, const int64_t* out_strides,
                                          float* lse, const int64_t* lse_strides, void* stream) {
-  return launch_attention({true, true, false}, q, q_strides, k, k_strides, value_tiles, indices,
+  return launch_attention({true, true, false}, q, q_strides, key_tiles, value_tiles, indices,
                           index_strides, counts, count_strides, mean_k, mean_v, block_counts,
                           batch, seq, q_heads, kv_heads, head_dim, block_size, scale, out,
                           out_strides, lse, lse_strides, stream);
@@ -513,7 +605,7 @@ extern "C" int spx_mean_tail(const void* q, const int64_t* q_strides, const int6
                              float* out, const int64_t* out_strides, float* lse,
                              const int64_t* lse_strides, void* stream) {
   SPX_REQUIRE(indices != nullptr, SPX_EINVAL, "mean_tail: indices must be given");
-  return launch_attention({false, true, true}, q, q_strides, nullptr, nullptr, nullptr, indices,
+  return launch_attention({false, true, true}, q, q_strides, nullptr, nullptr, indices,
                           index_strides, counts, count_strides, mean_k, mean_v, block_counts,
                           batch, seq, q_heads, kv_heads, head_dim, block_size, scale, out,
                           out_strides, lse, lse_strides, stream);

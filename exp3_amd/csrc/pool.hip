@@ -5,9 +5,11 @@
 //     fp32 sum over the valid rows / valid count, rounded to bf16;
 //   * fp32 descriptors (kernels.py:22-46): mean_k, var_k = max(0, E[k^2] - mean^2),
 //     mean_v, sigma_v = sqrt(sum_d max(0, E[v^2] - mean_v^2)), block counts;
-//   * value tiles for the attention kernel: V of the block transposed to
-//     [dim][128 key slots] with the key permutation of value_slot_of_key, keys
-//     past the sequence end zero.
+//   * attention tiles: the block's K rows and its V transposed to [dim][128 key
+//     slots] (key permutation of value_slot_of_key), rows / keys past the sequence
+//     end zero, each 128 x 128 bf16 tile stored with 16-byte chunk c of row r at
+//     position c ^ (r & 15). The attention kernel copies a tile into LDS verbatim
+//     (direct global->LDS loads) and reads MFMA operands bank-conflict free.
 //
 // Bandwidth-bound: each workgroup streams a 128 x 128 bf16 K tile and V tile with
 // 16-byte loads (each row is 256 contiguous bytes), reduces columns in registers,
@@ -28,6 +30,7 @@ struct PoolArgs {
   float* var_k;
   float* sigma_v;  // [B, NB, Hkv]
   int32_t* counts;  // [NB]
+  uint16_t* key_tiles;    // [B, Hkv, NB, 128, D]
   uint16_t* value_tiles;  // [B, Hkv, NB, D, 128]
 };
 
@@ -47,7 +50,7 @@ __device__ __forceinline__ void accumulate8(const u32x4& raw, float* sum, float*
 }
 
 // Sum a per-lane array of 8 floats over the 4 row groups of a wave (lanes that
-// differ in bits 4 and 5) .
+// differ in bits 4 and 5).
 __device__ __forceinline__ void reduce_row_groups(float* x) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -74,15 +77,19 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
   float sk[8] = {}, qk[8] = {}, sv[8] = {}, qv[8] = {};
   const uint16_t* kbase = a.k + b * a.ks_b + g * a.ks_h + (int64_t)c * 8;
   const uint16_t* vbase = a.v + b * a.vs_b + g * a.vs_h + (int64_t)c * 8;
+  const int64_t tile_off = ((((int64_t)b * a.kv_heads + g) * a.blocks + j) * kBlock) * kHeadDim;
 
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int row = rg * 8 + i;
     const bool valid = row < n;
     const int64_t token = (int64_t)j * kBlock + row;
-    if (DO_K && valid) {
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(kbase + token * a.ks_s);
-      accumulate8(raw, sk, qk);
+    if (DO_K || DO_TILES) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (valid) raw = *reinterpret_cast<const u32x4*>(kbase + token * a.ks_s);
+      if (DO_K && valid) accumulate8(raw, sk, qk);
+      if (DO_TILES)
+        *reinterpret_cast<u32x4*>(a.key_tiles + tile_off + row * kHeadDim + ((c ^ (row & 15)) << 3)) = raw;
     }
     if (DO_V || DO_TILES) {
       u32x4 raw = {0u, 0u, 0u, 0u};
@@ -135,10 +142,10 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
   if (a.counts && blockIdx.y == 0 && tid == 0) a.counts[j] = n;
 
   if (DO_TILES) {
-    // Transposed write-out: lane -> (dim row, 8-slot chunk); each thread gathers
-    // the 8 keys of its slots from the staged rows and stores 16 bytes.
-    uint16_t* tile = a.value_tiles +
-                     ((((int64_t)b * a.kv_heads + g) * a.blocks + j) * kHeadDim) * kBlock;
+    // Transposed write-out: thread -> (dim row d, 8-slot chunk); each gathers the
+    // 8 keys of its slots from the staged rows and stores 16 bytes at the swizzled
+    // chunk position.
+    uint16_t* tile = a.value_tiles + tile_off;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int id = tid + kPoolThreads * i;  // 0 .. 2047
@@ -155,7 +162,8 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
         const uint32_t hi = vrows[(key0 + 1) * kVPitch + d];
         w[m >> 1] = lo | (hi << 16);
       }
-      *reinterpret_cast<u32x4*>(tile + d * kBlock + chunk * 8) = u32x4{w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<u32x4*>(tile + d * kBlock + ((chunk ^ (d & 15)) << 3)) =
+          u32x4{w[0], w[1], w[2], w[3]};
     }
   }
   if (DO_V) {
@@ -183,28 +191,34 @@ extern "C" int spx_block_pool(const void* k, const int64_t* k_strides, const voi
                               const int64_t* v_strides, int batch, int seq, int kv_heads,
                               int head_dim, int block_size, void* mean_k_bf16, float* mean_k,
                               float* mean_v, float* var_k, float* sigma_v, int32_t* counts,
-                              void* value_tiles, void* stream) {
+                              void* key_tiles, void* value_tiles, void* stream) {
   SPX_REQUIRE(head_dim == kHeadDim, SPX_EUNSUPPORTED, "head_dim %d unsupported (only 128)", head_dim);
   SPX_REQUIRE(block_size == kBlock, SPX_EUNSUPPORTED, "block_size %d unsupported (only 128)", block_size);
   SPX_REQUIRE(batch > 0 && seq > 0 && kv_heads > 0, SPX_EINVAL,
               "batch, seq and kv_heads must be positive (got %d, %d, %d)", batch, seq, kv_heads);
+  SPX_REQUIRE((key_tiles == nullptr) == (value_tiles == nullptr), SPX_EINVAL,
+              "key_tiles and value_tiles are produced together");
   const bool do_k = mean_k_bf16 || mean_k || var_k;
   const bool do_v = mean_v || sigma_v;
   const bool do_tiles = value_tiles != nullptr;
-  if (do_k) { int e = check_tensor4("k", k, k_strides); if (e) return e; }
+  if (do_k || do_tiles) { int e = check_tensor4("k", k, k_strides); if (e) return e; }
   if (do_v || do_tiles) { int e = check_tensor4("v", v, v_strides); if (e) return e; }
-  if (!do_k && !do_v && !do_tiles) {
-    if (!counts) return SPX_OK;
+  if (do_tiles) {
+    SPX_REQUIRE((reinterpret_cast<uintptr_t>(key_tiles) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(value_tiles) & 15) == 0,
+                SPX_EINVAL, "key_tiles / value_tiles must be 16-byte aligned");
   }
+  if (!do_k && !do_v && !do_tiles && !counts) return SPX_OK;
   PoolArgs a{};
   a.k = static_cast<const uint16_t*>(k);
-  if (do_k) { a.ks_b = k_strides[0]; a.ks_s = k_strides[1]; a.ks_h = k_strides[2]; }
+  if (do_k || do_tiles) { a.ks_b = k_strides[0]; a.ks_s = k_strides[1]; a.ks_h = k_strides[2]; }
   a.v = static_cast<const uint16_t*>(v);
   if (do_v || do_tiles) { a.vs_b = v_strides[0]; a.vs_s = v_strides[1]; a.vs_h = v_strides[2]; }
   a.batch = batch; a.seq = seq; a.kv_heads = kv_heads; a.blocks = num_blocks(seq);
   a.mean_k_bf16 = static_cast<uint16_t*>(mean_k_bf16);
   a.mean_k = mean_k; a.mean_v = mean_v; a.var_k = var_k; a.sigma_v = sigma_v;
   a.counts = counts;
+  a.key_tiles = static_cast<uint16_t*>(key_tiles);
   a.value_tiles = static_cast<uint16_t*>(value_tiles);
   dim3 grid(a.blocks, batch * kv_heads);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -228,7 +242,7 @@ extern "C" int spx_block_mean_k(const void* k, const int64_t* k_strides, int bat
   SPX_REQUIRE(mean_k != nullptr, SPX_EINVAL, "mean_k: null pointer");
   return spx_block_pool(k, k_strides, nullptr, nullptr, batch, seq, kv_heads, head_dim,
                         block_size, mean_k, nullptr, nullptr, nullptr, nullptr, nullptr,
-                        nullptr, stream);
+                        nullptr, nullptr, stream);
 }
 
 extern "C" int spx_block_descriptors(const void* k, const int64_t* k_strides, const void* v,
@@ -238,5 +252,5 @@ extern "C" int spx_block_descriptors(const void* k, const int64_t* k_strides, co
   SPX_REQUIRE(mean_k && mean_v && var_k && sigma_v && counts, SPX_EINVAL,
               "block_descriptors: every output must be given");
   return spx_block_pool(k, k_strides, v, v_strides, batch, seq, kv_heads, head_dim, block_size,
-                        nullptr, mean_k, mean_v, var_k, sigma_v, counts, nullptr, stream);
+                        nullptr, mean_k, mean_v, var_k, sigma_v, counts, nullptr, nullptr, stream);
 }

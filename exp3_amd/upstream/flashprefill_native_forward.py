@@ -87,18 +87,24 @@ def deal_output_score(score: torch.Tensor, attention_sink: int, window: int,
     return indices, counts
 
 
-def value_tiles(v: torch.Tensor, block_size: int = 128) -> torch.Tensor:
-    """Transposed, key-permuted per-block V tiles the attention kernel reads
-    (``[B, Hkv, NB, D, 128]`` bf16); produced by the pooling pass."""
-    device = _lib.require_gpu(v)
+def attention_tiles(k: torch.Tensor, v: torch.Tensor, block_size: int = 128):
+    """Per-block K and V tiles the attention kernel copies into LDS verbatim:
+    key tiles ``[B, Hkv, NB, 128, D]`` and value tiles ``[B, Hkv, NB, D, 128]``
+    (V transposed, keys permuted), zero past the sequence end, 16-byte chunks
+    XOR-swizzled by row; produced by the pooling pass."""
+    device = _lib.require_gpu(k, v)
+    k = _lib.kernel_view(k)
     v = _lib.kernel_view(v)
     batch, sequence, kv_heads, head_dim = v.shape
-    tiles = torch.empty(batch, kv_heads, _blocks(sequence, block_size), head_dim, block_size,
-                        dtype=torch.bfloat16, device=device)
-    _lib.call("spx_block_pool", None, None, _lib.ptr(v), _lib.strides(v), batch, sequence,
-              kv_heads, head_dim, block_size, None, None, None, None, None, None,
-              _lib.ptr(tiles), _lib.stream(device))
-    return tiles
+    blocks = _blocks(sequence, block_size)
+    key_tiles = torch.empty(batch, kv_heads, blocks, block_size, head_dim, dtype=torch.bfloat16,
+                            device=device)
+    value_tiles = torch.empty(batch, kv_heads, blocks, head_dim, block_size, dtype=torch.bfloat16,
+                              device=device)
+    _lib.call("spx_block_pool", _lib.ptr(k), _lib.strides(k), _lib.ptr(v), _lib.strides(v), batch,
+              sequence, kv_heads, head_dim, block_size, None, None, None, None, None, None,
+              _lib.ptr(key_tiles), _lib.ptr(value_tiles), _lib.stream(device))
+    return key_tiles, value_tiles
 
 
 @torch.no_grad()
@@ -116,11 +122,11 @@ def exact_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("indices must be int64 and counts int32")
     batch, sequence, q_heads, head_dim = q.shape
     check_attention_shapes(q, k, v, indices, counts, block_size)
-    tiles = value_tiles(v, block_size)
+    key_tiles, value_tiles = attention_tiles(k, v, block_size)
     output = torch.empty(batch, sequence, q_heads, head_dim, dtype=q.dtype, device=device)
     lse = torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
-    _lib.call("spx_exact_attention", _lib.ptr(q), _lib.strides(q), _lib.ptr(k), _lib.strides(k),
-              _lib.ptr(tiles), _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
+    _lib.call("spx_exact_attention", _lib.ptr(q), _lib.strides(q), _lib.ptr(key_tiles),
+              _lib.ptr(value_tiles), _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
               _lib.strides(counts), batch, sequence, q_heads, k.shape[2], head_dim, block_size,
               float(scale), _lib.ptr(output), _lib.strides(output), _lib.ptr(lse),
               _lib.strides(lse), _lib.stream(device))

@@ -37,7 +37,7 @@ extern "C" {
 #define SPX_EUNSUPPORTED (-2) /* valid in the reference, not built here       */
 #define SPX_ELAUNCH (-3)      /* HIP launch / runtime failure                 */
 
-#define SPX_ABI_VERSION 1
+#define SPX_ABI_VERSION 2
 
 /* Selector ids for spx_selector_scores (kernels.py:62). */
 #define SPX_SELECTOR_MEAN_BALANCED 0
@@ -67,16 +67,20 @@ int spx_block_descriptors(const void* k, const int64_t* k_strides, const void* v
 
 /* One pass over K and V producing any subset of: bf16 mean K (as
  * spx_block_mean_k), the FP32 descriptors (as spx_block_descriptors) and the
- * value tiles the attention entry points read. Null outputs are skipped.
+ * attention tiles the attention entry points read. Null outputs are skipped;
+ * key_tiles and value_tiles are produced together.
+ * key_tiles:   [B, Hkv, NB, 128, D] bf16, the block's K rows;
  * value_tiles: [B, Hkv, NB, D, 128] bf16, V transposed per block with the key
- * permutation documented in exp3_amd/csrc/common.h; keys past seq are zero.
+ *              permutation documented in exp3_amd/csrc/common.h.
+ * Rows / keys past seq are zero, and inside every 128 x 128 tile the 16-byte
+ * chunk c of row r is stored at chunk position c ^ (r & 15) (the LDS layout).
  * Fuses kernels.py:22-46 with upstream/flashprefill_native_forward.py:420-442
  * (the descriptor stage of attention.py:80-86). */
 int spx_block_pool(const void* k, const int64_t* k_strides, const void* v,
                    const int64_t* v_strides, int batch, int seq, int kv_heads,
                    int head_dim, int block_size, void* mean_k_bf16, float* mean_k,
                    float* mean_v, float* var_k, float* sigma_v, int32_t* counts,
-                   void* value_tiles, void* stream);
+                   void* key_tiles, void* value_tiles, void* stream);
 
 /* ------------------------------------------------------------- routing */
 
@@ -145,14 +149,14 @@ int spx_selector_scores(const void* q, const int64_t* q_strides, const float* me
 /* ----------------------------------------------------------- attention */
 
 /* Block-sparse causal flash attention over each (query tile, head)'s index list.
- * value_tiles come from spx_block_pool. indices: int64 [B, NB, NB, Hq] (strided),
+ * key_tiles / value_tiles come from spx_block_pool. indices: int64 [B, NB, NB, Hq] (strided),
  * counts: int32 [B, NB, Hq] (strided); indices == NULL selects every causal block
  * (dense causal attention). out: bf16 [B, S, Hq, D] (strided); lse: natural-log LSE
  * fp32 [B, S, Hq] (strided, may be NULL).
  * Replaces upstream/flashprefill_native_forward.py:478-521 (exact_attention) and the
  * Triton kernel _flash_forward (:215-354). */
-int spx_exact_attention(const void* q, const int64_t* q_strides, const void* k,
-                        const int64_t* k_strides, const void* value_tiles,
+int spx_exact_attention(const void* q, const int64_t* q_strides, const void* key_tiles,
+                        const void* value_tiles,
                         const int64_t* indices, const int64_t* index_strides,
                         const int32_t* counts, const int64_t* count_strides, int batch,
                         int seq, int q_heads, int kv_heads, int head_dim, int block_size,
@@ -167,8 +171,8 @@ int spx_exact_attention(const void* q, const int64_t* q_strides, const void* k,
  * Replaces the exact + mean + merge stages of attention.py:253-305:
  * upstream exact_attention, kernels.py:179-230 (mean_tail) and kernels.py:312-325
  * (merge_exact_mean). */
-int spx_sparse_attention_mean(const void* q, const int64_t* q_strides, const void* k,
-                              const int64_t* k_strides, const void* value_tiles,
+int spx_sparse_attention_mean(const void* q, const int64_t* q_strides, const void* key_tiles,
+                              const void* value_tiles,
                               const int64_t* indices, const int64_t* index_strides,
                               const int32_t* counts, const int64_t* count_strides,
                               const float* mean_k, const float* mean_v,

@@ -54,19 +54,32 @@ def test_block_descriptors(gpu, length):
 
 
 @pytest.mark.parametrize("length", (257, 1089))
-def test_value_tiles_layout(gpu, length):
+def test_attention_tiles_layout(gpu, length):
+    """Key tiles hold K rows, value tiles V transposed with the documented key
+    permutation; chunk c of row r sits at chunk position c ^ (r & 15); zero past S."""
     q, k, v = inputs(length, seed=5)
-    vg, = _gpu(v)
-    tiles = to_np(up.value_tiles(vg))          # [B, Hkv, NB, D, 128]
-    vv = to_np(v)
-    blocks = tiles.shape[2]
-    for slot in range(128):
-        c16, s = divmod(slot, 16)
-        key = c16 * 16 + 4 * (s // 8) + (s % 4) + 8 * ((s % 8) // 4)
-        for j in range(blocks):
-            token = j * 128 + key
-            want = vv[:, token].transpose(0, 1, 2) if token < length else np.zeros_like(vv[:, 0])
-            np.testing.assert_array_equal(tiles[:, :, j, :, slot], want)
+    kg, vg = _gpu(k, v)
+    kt, vt = (to_np(x) for x in up.attention_tiles(kg, vg))   # [B, Hkv, NB, 128, 128]
+    blocks = kt.shape[2]
+
+    def unswizzle(tile):
+        out = np.empty_like(tile)
+        for r in range(128):
+            for c in range(16):
+                out[..., r, c * 8:(c + 1) * 8] = tile[..., r, (c ^ (r & 15)) * 8:((c ^ (r & 15)) + 1) * 8]
+        return out
+
+    kt, vt = unswizzle(kt), unswizzle(vt)
+    kk, vv = to_np(k), to_np(v)
+    pad = blocks * 128 - length
+    kp = np.concatenate([kk, np.zeros((1, pad) + kk.shape[2:], np.float32)], axis=1)
+    vp = np.concatenate([vv, np.zeros((1, pad) + vv.shape[2:], np.float32)], axis=1)
+    want_k = kp.reshape(1, blocks, 128, 4, 128).transpose(0, 3, 1, 2, 4)
+    np.testing.assert_array_equal(kt, want_k)
+    key_of_slot = np.array([(s // 16) * 16 + 4 * ((s % 16) // 8) + (s % 4) + 8 * ((s % 8) // 4)
+                            for s in range(128)])
+    want_v = vp.reshape(1, blocks, 128, 4, 128)[:, :, key_of_slot].transpose(0, 3, 1, 4, 2)
+    np.testing.assert_array_equal(vt, want_v)
 
 
 @pytest.mark.parametrize("length", (257, 1089, 4096))
