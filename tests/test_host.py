@@ -48,7 +48,7 @@ def test_c_abi_argument_validation_without_gpu():
     assert lib.spx_selector_scores(fake, s4, fake, fake, fake, fake, 1, 256, 28, 4, 128, 128, 7,
                                    ctypes.c_float(0.1), fake, s4, None) == _lib.SPX_EINVAL
     # 28 q heads over 3 kv heads is not a GQA grouping
-    assert lib.spx_exact_attention(fake, s4, fake, s4, fake, None, None, None, None, 1, 256, 28, 3,
+    assert lib.spx_exact_attention(fake, s4, fake, fake, None, None, None, None, 1, 256, 28, 3,
                                    128, 128, ctypes.c_float(0.1), fake, s4, None, None,
                                    None) == _lib.SPX_EINVAL
     # 131073 tokens exceed the 1024-block limit of the routing kernels
