@@ -13,9 +13,11 @@
 // (mean_tail) and :312-325 (merge_exact_mean).
 //
 // gfx950 design
-//   * One workgroup (4 waves, 32 query rows each) per (query tile, q head); two
-//     workgroups per CU (66 KB LDS each), so one's tile loads and barriers overlap
-//     the other's math.
+//   * One workgroup (8 waves) per (pair of adjacent query tiles t, t - 1; q head):
+//     waves 0-3 own the 128 rows of tile t, waves 4-7 those of tile t - 1, 32 rows
+//     each. The two tiles' block lists are merged, so every K/V tile copied into
+//     LDS serves both (the lists differ by little: sinks, window and most routed
+//     blocks are shared).
 //   * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16:
 //     each lane owns one query column, so row max / row sum are in-lane reductions
 //     plus one exchange with the other lane half, the O rescale is a per-lane
@@ -23,19 +25,24 @@
 //     O^T = V^T P^T (no shuffles, no LDS round trip for P).
 //   * K rows and the pre-transposed value tile come from the pooling pass already
 //     in LDS order (XOR-swizzled 16-byte chunks, conflict-free operand reads) and
-//     are copied with direct global->LDS loads (no staging registers). Operand
-//     reads are issued one MFMA step ahead.
-//   * Full blocks run without masks; on the diagonal block wave w touches only key
-//     sub-blocks 0 .. w. The running max moves lazily (only by more than 2^8), so
-//     the O rescale is a rarely taken wave-uniform branch.
-//   * Grid order: (tile, kv group) pairs heaviest-first, and the heads of one group
-//     consecutive on the same XCD (workgroup i runs on XCD i % 8), so the seven q
-//     heads sharing a KV block read it from the same L2.
+//     are copied with direct global->LDS loads into double buffers: block u + 1
+//     lands while block u is computed.
+//   * Full blocks are software-pipelined over their four 32-key sub-blocks (matrix
+//     work of one sub-block around the exponentials of the previous one); the
+//     running max moves lazily (only by more than 2^8), so the O rescale is a
+//     rarely taken wave-uniform branch. The diagonal blocks (t and t - 1) run last
+//     through a masked path in which wave w touches only key sub-blocks 0 .. w.
+//   * Grid order: (tile pair, kv group) items heaviest-first, and the heads of one
+//     group consecutive on the same XCD (workgroup i runs on XCD i % 8), so the
+//     seven q heads sharing a KV block read it from the same L2.
+#include <type_traits>
+
 #include "common.h"
 
 namespace spx {
 
-constexpr int kAttnThreads = 256;     // 4 waves x 32 query rows
+constexpr int kAttnThreads = 512;     // 8 waves: two query tiles x 4 waves x 32 rows
+constexpr int kItemWaves = 4;        // waves per query tile
 constexpr int kMaxBlocksAttn = 1024;
 constexpr int kTailTile = 64;        // mean keys per tail tile (hi and lo rows fill K LDS)
 constexpr float kLazyRescale = 8.0f; // log2 headroom before a column's running max moves
@@ -87,18 +94,42 @@ struct WaveState {
 
 // Copy one 32 KB tile, already in LDS order in global memory, into LDS with
 // direct global->LDS loads: lane l of a wave lands at (wave base) + 16 l, so
-// thread id moves 16-byte chunks id + 256 i. No VGPRs are used for staging;
+// thread id moves 16-byte chunks id + 512 i. No VGPRs are used for staging;
 // completion is awaited with wait_tiles() before the publishing barrier.
+//
+// The loads are issued from inline assembly on purpose: the compiler tracks a
+// builtin LDS-DMA load as a pending write to all of LDS and then waits for it
+// before the next LDS read, which would serialise the copy of block u + 1 with
+// the math on block u (they use different buffers). The only consumer waits
+// explicitly (wait_tiles, then a barrier).
+__device__ __forceinline__ void dma_part(const uint16_t* src, uint16_t* lds, int tid, int i);
+
 __device__ __forceinline__ void dma_tile(const uint16_t* src, uint16_t* lds, int tid) {
-  const int w = tid >> 6, lane = tid & 63;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int chunk0 = i * kAttnThreads + w * 64;
-    const uint16_t* g = src + (int64_t)(chunk0 + lane) * 8;
-    uint16_t* l = lds + chunk0 * 8;
-    __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)g,
-                                     (void __attribute__((address_space(3)))*)l, 16, 0, 0);
-  }
+  for (int i = 0; i < 4; ++i) dma_part(src, lds, tid, i);
+}
+
+// Part i (0..3) of dma_tile: one quarter of the tile's 16-byte chunks.
+// The part offset goes into the scalar base, so every part uses the same per-lane
+// offset tid * 16 (one VGPR for all copies).
+__device__ __forceinline__ void dma_part(const uint16_t* src, uint16_t* lds, int tid, int i) {
+  const int w = tid >> 6;
+  const uint32_t lds_base =
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)lds;
+  const int chunk0 = i * kAttnThreads + w * 64;
+  const uint32_t voff = (uint32_t)tid * 16u;
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_base + (uint32_t)chunk0 * 16u);
+  src += i * kAttnThreads * 8;
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m0), "v"(voff), "s"(src)
+      : "memory");
 }
 
 __device__ __forceinline__ void wait_tiles() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
@@ -183,8 +214,13 @@ __device__ __forceinline__ void softmax(f32x16 (&s)[4], WaveState& ws, float sca
   const float m_new = (mxs > ws.m + kLazyRescale) ? mxs : ws.m;
   if (__any(m_new != ws.m)) {
     const float corr = (m_new == ws.m) ? 1.0f : exp2_fast(ws.m - m_new);
+    // in place (tied operands): O keeps its registers across the rarely taken
+    // branch instead of being copied into a second set on every block
 #pragma unroll
-    for (int db = 0; db < 4; ++db) ws.o[db] *= corr;
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(ws.o[db][r]) : "v"(corr));
+    }
     ws.l *= corr;
     ws.m = m_new;
   }
@@ -241,27 +277,211 @@ __device__ __forceinline__ void exact_block(const uint16_t* kb, const uint16_t* 
   accumulate_pv<2 * NMB>(vb, ws, pb);
 }
 
-// Ascending compaction of flagged ids into LDS `list`; returns the count (all threads).
-__device__ __forceinline__ int compact_append(bool flag, int id, int16_t* list, int base,
-                                             int* wave_counts) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int nwaves = kAttnThreads / 64;
-  const uint64_t ballot = __ballot(flag);
-  const int before = __popcll(ballot & ((1ull << lane) - 1ull));
-  if (lane == 0) wave_counts[w] = __popcll(ballot);
-  __syncthreads();
-  int offset = base;
-  for (int x = 0; x < w; ++x) offset += wave_counts[x];
-  if (flag) list[offset + before] = (int16_t)id;
-  int total = base;
-  for (int x = 0; x < nwaves; ++x) total += wave_counts[x];
-  __syncthreads();
-  return total;
+// ---------------------------------------------------------------- full blocks
+// A full (unmasked) block, software-pipelined over its four 32-key sub-blocks so
+// that one wave overlaps its own exponentials with its matrix work:
+//
+//   step 0: scores S0
+//   step k: P V of sub-block k-2 | max of S(k-1) | rescale | scores S(k) with the
+//           exponentials of S(k-1) in between            (k = 1..4, as they exist)
+//   step 5: P V of sub-block 3
+//
+// The running max moves lazily per sub-block (only when a column's scaled max
+// exceeds it by more than 2^8); the rescale of O comes after the P V products that
+// used the old max were issued and before any that use the new one.
+//
+// LDS operand addresses: entry c of a table is the byte address of 16-byte chunk
+// pair c of this lane's operand row in tile buffer 0; row 32 i + col of buffer B is
+// the same entry plus the immediate B * 32 KB + i * 8 KB (rows congruent mod 16
+// share the swizzle), so no address arithmetic is left in the block.
+struct OperandTables {
+  uint32_t k[8];
+  uint32_t v[8];
+};
+
+__device__ __forceinline__ uint32_t lds_address(const uint16_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)p;
+}
+
+__device__ __forceinline__ bf16x8 lds_at(uint32_t byte_address) {
+  const u32x4 v =
+      *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>((uintptr_t)byte_address);
+  return as_bf16x8(v);
+}
+
+__device__ __forceinline__ OperandTables operand_tables(const uint16_t* k0, const uint16_t* v0) {
+  OperandTables t;
+  const int e0 = operand_base(threadIdx.x & 31);
+  const uint32_t kb = lds_address(k0), vb = lds_address(v0);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const uint32_t off = (uint32_t)(e0 ^ (c << 4)) * 2u;
+    t.k[c] = (uint32_t)opaque((int)(kb + off));
+    t.v[c] = (uint32_t)opaque((int)(vb + off));
+  }
+  return t;
+}
+
+constexpr uint32_t kTileBytes = kBlock * kHeadDim * 2;  // one 32 KB K or V tile
+constexpr uint32_t kRowGroupBytes = 32 * kBlock * 2;    // 32 operand rows
+
+// key operands of sub-block mb (dim chunks 0..7)
+template <int BUF>
+__device__ __forceinline__ void sub_keys(const OperandTables& tb, int mb, bf16x8 (&r)[8]) {
+#pragma unroll
+  for (int dc = 0; dc < 8; ++dc) r[dc] = lds_at(tb.k[dc] + BUF * kTileBytes + mb * kRowGroupBytes);
+}
+
+// scores of one sub-block: S^T = K_mb Q^T (8 chained MFMAs over the dim chunks)
+__device__ __forceinline__ void sub_scores(const bf16x8 (&r)[8], const WaveState& ws, f32x16& acc) {
+  acc = f32x16{};
+#pragma unroll
+  for (int dc = 0; dc < 8; ++dc) acc = mfma32(r[dc], ws.qb[dc], acc);
+}
+
+// value operands of sub-block j: value chunks 2j, 2j+1 of every dim block
+template <int BUF>
+__device__ __forceinline__ void sub_values(const OperandTables& tb, int j, bf16x8 (&r)[8]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+      r[h * 4 + db] = lds_at(tb.v[2 * j + h] + BUF * kTileBytes + db * kRowGroupBytes);
+}
+
+__device__ __forceinline__ void sub_pv(const bf16x8 (&r)[8], const bf16x8 (&p)[2], WaveState& ws) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int db = 0; db < 4; ++db) ws.o[db] = mfma32(r[h * 4 + db], p[h], ws.o[db]);
+}
+
+// column max of one sub-block (both lane halves hold keys of the same column)
+__device__ __forceinline__ float sub_max(const f32x16& sv) {
+  float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
+#pragma unroll
+  for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sv[r]), sv[r + 1]);
+  mx = fmaxf(mx, sv[15]);
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false,
+                                                   false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+
+__device__ __forceinline__ void lazy_rescale(WaveState& ws, float mxs) {
+  const bool move = mxs > ws.m + kLazyRescale;
+  if (__any(move)) {
+    const float m_new = move ? mxs : ws.m;
+    const float corr = move ? exp2_fast(ws.m - m_new) : 1.0f;
+    // in place (tied operands): O keeps its registers across the rarely taken branch
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(ws.o[db][r]) : "v"(corr));
+    }
+    ws.l *= corr;
+    ws.m = m_new;
+  }
+}
+
+// acc + lo + hi of a packed bf16 pair (v_dot2_f32_bf16 with (1, 1); issued from
+// assembly because the compiler's dot2 builtin lowering reads the wrong register
+// when several of them are chained)
+__device__ __forceinline__ float add_bf16_pair(float acc, uint32_t pair) {
+  asm("v_dot2_f32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(pair), "s"(0x3f803f80u));
+  return acc;
+}
+
+// probabilities of one sub-block as bf16 B operands; the running sum adds the
+// rounded values (the ones the P V product uses)
+__device__ __forceinline__ void sub_exp(const f32x16& sv, WaveState& ws, float scale,
+                                        bf16x8 (&p)[2]) {
+  const float neg_m = -ws.m;
+  float l = ws.l;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = exp2_fast(fmaf(sv[8 * h + 2 * i], scale, neg_m));
+      const float b = exp2_fast(fmaf(sv[8 * h + 2 * i + 1], scale, neg_m));
+      w[i] = pack_bf16x2(a, b);
+      l = add_bf16_pair(l, w[i]);
+    }
+    p[h] = as_bf16x8(w);
+  }
+  ws.l = l;
+}
+
+// The copy of the next block: source tiles and the other buffers.
+struct NextCopy {
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* kd;
+  uint16_t* vd;
+  bool any;
+};
+
+template <int BUF>
+__device__ __forceinline__ void full_block(const OperandTables& tb, WaveState& ws, float scale) {
+  f32x16 s[2];
+  bf16x8 p[2][2];
+  bf16x8 rv[8], rk[8];
+  // Each operand group is read one MFMA group ahead: the key reads of step k land
+  // during the P V products of step k, the value reads for step k + 1 during the
+  // scores of step k.
+  sub_keys<BUF>(tb, 0, rk);
+  fence();
+  sub_scores(rk, ws, s[0]);
+#pragma unroll
+  for (int k = 1; k <= 5; ++k) {
+    fence();
+    if (k <= 3) sub_keys<BUF>(tb, k, rk);
+    fence();
+    float mx = 0.0f;
+    if (k <= 4) mx = sub_max(s[(k - 1) & 1]);
+    if (k >= 2) sub_pv(rv, p[(k - 2) & 1], ws);
+    if (k <= 4) {
+      lazy_rescale(ws, mx * scale);
+      fence();
+      sub_values<BUF>(tb, k - 1, rv);
+      fence();
+      if (k <= 3) sub_scores(rk, ws, s[k & 1]);
+      sub_exp(s[(k - 1) & 1], ws, scale, p[(k - 1) & 1]);
+    }
+  }
+}
+
+// Mean-correction tail tile: stage up to kTailTile unselected blocks (ids from
+// `ids`) of one query tile into kb / vb (K hi rows i, lo rows 64 + i; value slots
+// 0..63), with per-key biases ln(n_j) log2 e. Threads of one item (128 lanes
+// stride `stride`) cooperate.
+__device__ __forceinline__ void stage_tail(const AttnArgs& a, const int16_t* ids, int ntail, int t0,
+                                           int64_t desc_base, uint16_t* kb, uint16_t* vb,
+                                           float* bias, int tid0, int stride) {
+  for (int e = tid0; e < kTailTile * kHeadDim; e += stride) {
+    const int i = e >> 7, d = e & 127;
+    const int j = (t0 + i < ntail) ? (int)ids[t0 + i] : -1;
+    float mk = 0.0f, mv = 0.0f;
+    if (j >= 0) {
+      const int64_t off = (desc_base + (int64_t)j * a.kv_heads) * kHeadDim + d;
+      mk = a.mean_k[off];
+      mv = a.mean_v[off];
+    }
+    const uint16_t hi = to_bf16_bits(mk);
+    const uint16_t lo = to_bf16_bits(mk - __uint_as_float((uint32_t)hi << 16));
+    kb[swz(i, d >> 3) + (d & 7)] = hi;
+    kb[swz(kTailTile + i, d >> 3) + (d & 7)] = lo;
+    const int slot = value_slot_of_key(i);
+    vb[swz(d, slot >> 3) + (slot & 7)] = to_bf16_bits(mv);
+    if (d == 0) bias[i] = j >= 0 ? logf((float)a.bcounts[j]) * kLog2e : -INFINITY;
+  }
 }
 
 template <bool EXACT, bool TAIL, bool OUT_F32>
-__global__ __launch_bounds__(kAttnThreads, 2) void attn_kernel(AttnArgs a) {
-  // ---- work item: heaviest (tile, kv group) pairs first, group heads on one XCD
+__global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
+  // ---- work item: query tiles (t, t - 1) of one q head. Tile pairs heaviest first,
+  // the heads of one kv group consecutive on the same XCD (workgroup i runs on
+  // XCD i % 8) so the seven q heads sharing a KV block read it from one L2.
   const int p = blockIdx.x;
   const int xcd = p & 7;
   const int local = p >> 3;
@@ -270,34 +490,43 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_kernel(AttnArgs a) {
   const int pair = pair_local * 8 + xcd;
   if (pair >= a.num_pairs) return;
   const int bg = a.batch * a.kv_heads;
-  const int t = a.blocks - 1 - pair / bg;
+  const int tp = pair / bg;                          // tile pair: tiles NB-1-2tp, NB-2-2tp
   const int b = (pair % bg) / a.kv_heads;
   const int g = (pair % bg) % a.kv_heads;
   const int h = g * a.group + hg;
 
-  __shared__ __align__(16) uint16_t kbuf[kBlock * kBlock];
-  __shared__ __align__(16) uint16_t vbuf[kBlock * kBlock];
-  __shared__ int16_t blist[kMaxBlocksAttn];
-  __shared__ uint32_t listed[kMaxBlocksAttn / 32];
-  __shared__ float tail_bias[kTailTile];
+  __shared__ __align__(16) uint16_t kbuf[2][kBlock * kBlock];
+  __shared__ __align__(16) uint16_t vbuf[2][kBlock * kBlock];
+  __shared__ int16_t ulist[kMaxBlocksAttn];          // union of both lists, ascending
+  __shared__ uint8_t uflag[kMaxBlocksAttn];          // bit i: block listed for item i
+  __shared__ uint32_t bits[2][kMaxBlocksAttn / 32];  // per-item membership
+  __shared__ float tail_bias[2][kTailTile];
   __shared__ int wave_counts[kAttnThreads / 64];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int item = w >> 2;                           // 0: tile t, 1: tile t - 1
+  const int wi = w & 3;                              // wave inside its item
   const int col = lane & 31, half = lane >> 5;
-  const int q_pos = w * 32 + col;  // this lane's query inside the tile
+  const int q_pos = wi * 32 + col;                   // this lane's query inside its tile
   const float scale = a.scale_log2;
+  const int t_item[2] = {a.blocks - 1 - 2 * tp, a.blocks - 2 - 2 * tp};
+  const int t = t_item[item];                        // may be -1 (odd tile count)
+  const bool live = t >= 0;
 
   WaveState ws;
   {
     const int64_t qrow = (int64_t)t * kBlock + q_pos;
     const uint16_t* src = a.q + b * a.qs_b + qrow * a.qs_s + h * a.qs_h + half * 8;
-    const bool ok = qrow < a.seq;
+    const bool ok = live && qrow < a.seq;
 #pragma unroll
     for (int dc = 0; dc < 8; ++dc) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (ok) raw = *reinterpret_cast<const u32x4*>(src + dc * 16);
+      // consume the load here: the tile copies issued later share its counter,
+      // and a first use inside the block loop would wait for them every block
+      asm volatile("" : "+v"(raw));
       ws.qb[dc] = as_bf16x8(raw);
     }
     ws.m = -INFINITY;
@@ -306,91 +535,160 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_kernel(AttnArgs a) {
     for (int db = 0; db < 4; ++db) ws.o[db] = f32x16{};
   }
 
-  // ---- the tile's block list (valid ids, in list order) in LDS
-  int n = 0;
-  if (a.idx) {
-    int count = a.cnt[b * a.cs_b + t * a.cs_t + h * a.cs_h];
-    count = min(max(count, 0), a.blocks);
-    const int64_t* list = a.idx + b * a.is_b + t * a.is_t + h * a.is_h;
-    for (int p0 = 0; p0 < count; p0 += kAttnThreads) {
-      const int pos = p0 + tid;
-      int j = -1;
-      if (pos < count) j = (int)list[pos * a.is_p];
-      n = compact_append(pos < count && j >= 0 && j < a.blocks, j, blist, n, wave_counts);
+  // ---- membership bitmaps of both items' lists (valid ids), then their union
+  if (tid < 2 * (kMaxBlocksAttn / 32)) (&bits[0][0])[tid] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int tt = t_item[it];
+    if (tt < 0) continue;
+    if (a.idx) {
+      int count = a.cnt[b * a.cs_b + tt * a.cs_t + h * a.cs_h];
+      count = min(max(count, 0), a.blocks);
+      const int64_t* list = a.idx + b * a.is_b + tt * a.is_t + h * a.is_h;
+      for (int pos = tid; pos < count; pos += kAttnThreads) {
+        const int j = (int)list[pos * a.is_p];
+        if (j >= 0 && j < a.blocks) atomicOr(&bits[it][j >> 5], 1u << (j & 31));
+      }
+    } else {
+      for (int j = tid; j <= tt; j += kAttnThreads) atomicOr(&bits[it][j >> 5], 1u << (j & 31));
     }
-  } else {
-    n = t + 1;
-    for (int j = tid; j <= t; j += kAttnThreads) blist[j] = (int16_t)j;
-    __syncthreads();
   }
-  n = __builtin_amdgcn_readfirstlane(n);
+  __syncthreads();
+  // Processing order: every listed block except the two diagonal ones (t, t - 1),
+  // ascending, then the diagonal ones. The block loop for the first part has a
+  // single (unmasked) code path, which keeps O in one register set.
+  int nu = 0;
+  auto compact = [&](bool diagonal_pass) {
+    for (int j0 = 0; j0 < a.blocks; j0 += kAttnThreads) {
+      const int j = j0 + tid;
+      int f = 0;
+      if (j < a.blocks && ((j == t_item[0] || j == t_item[1]) == diagonal_pass))
+        f = ((bits[0][j >> 5] >> (j & 31)) & 1u) | (((bits[1][j >> 5] >> (j & 31)) & 1u) << 1);
+      const bool flag = f != 0;
+      const uint64_t ballot = __ballot(flag);
+      const int before = __popcll(ballot & ((1ull << lane) - 1ull));
+      if (lane == 0) wave_counts[w] = __popcll(ballot);
+      __syncthreads();
+      int offset = nu;
+      for (int x = 0; x < w; ++x) offset += wave_counts[x];
+      if (flag) {
+        ulist[offset + before] = (int16_t)j;
+        uflag[offset + before] = (uint8_t)f;
+      }
+      for (int x = 0; x < kAttnThreads / 64; ++x) nu += wave_counts[x];
+      __syncthreads();
+    }
+  };
+  compact(false);
+  const int n_full = __builtin_amdgcn_readfirstlane(nu);
+  compact(true);
+  nu = __builtin_amdgcn_readfirstlane(nu);
 
-  if (EXACT) {
+  if (EXACT && nu > 0) {
     const int64_t tile_elems = (int64_t)kBlock * kHeadDim;
     const uint16_t* kbase = a.kt + (((int64_t)b * a.kv_heads + g) * a.blocks) * tile_elems;
     const uint16_t* vbase = a.vt + (((int64_t)b * a.kv_heads + g) * a.blocks) * tile_elems;
-    for (int i = 0; i < n; ++i) {
-      const int j = __builtin_amdgcn_readfirstlane(blist[i]);
-      dma_tile(kbase + j * tile_elems, kbuf, tid);
-      dma_tile(vbase + j * tile_elems, vbuf, tid);
+    {
+      const int j0 = __builtin_amdgcn_readfirstlane(ulist[0]);
+      dma_tile(kbase + j0 * tile_elems, kbuf[0], tid);
+      dma_tile(vbase + j0 * tile_elems, vbuf[0], tid);
+    }
+    // Publish block u (its copy was issued one step earlier) and start the copy of
+    // block u + 1 into the other buffers, where it lands during block u's math.
+    auto begin_block = [&](int u) {
       wait_tiles();
-      __syncthreads();
-      if (j != t) {
-        exact_block<4, false>(kbuf, vbuf, ws, scale, q_pos);
-      } else {
-        switch (w) {  // wave w reaches key sub-blocks 0 .. w of the diagonal block
-          case 0: exact_block<1, true>(kbuf, vbuf, ws, scale, q_pos); break;
-          case 1: exact_block<2, true>(kbuf, vbuf, ws, scale, q_pos); break;
-          case 2: exact_block<3, true>(kbuf, vbuf, ws, scale, q_pos); break;
-          default: exact_block<4, true>(kbuf, vbuf, ws, scale, q_pos); break;
+      __syncthreads();  // block u visible to all; every wave is done with block u - 1
+      if (u + 1 < nu) {
+        const int jn = __builtin_amdgcn_readfirstlane(ulist[u + 1]);
+        dma_tile(kbase + jn * tile_elems, kbuf[(u + 1) & 1], tid);
+        dma_tile(vbase + jn * tile_elems, vbuf[(u + 1) & 1], tid);
+      }
+    };
+    const OperandTables tables = operand_tables(kbuf[0], vbuf[0]);
+    int u = 0;
+    // Full blocks: publish block u, then run it while its successor is copied (by
+    // full_block, spread over its steps; here at once if this item skips block u).
+    auto run_full = [&](int uu, auto buf) {
+      constexpr int B = decltype(buf)::value;
+      const int f = __builtin_amdgcn_readfirstlane(uflag[uu]);
+      wait_tiles();
+      __syncthreads();  // block uu visible to all; every wave is done with block uu - 1
+      NextCopy nx;
+      nx.any = uu + 1 < nu;
+      const int jn = nx.any ? __builtin_amdgcn_readfirstlane(ulist[uu + 1]) : 0;
+      nx.k = kbase + jn * tile_elems;
+      nx.v = vbase + jn * tile_elems;
+      nx.kd = kbuf[B ^ 1];
+      nx.vd = vbuf[B ^ 1];
+      if (nx.any) {  // block uu + 1 lands in the other buffers during block uu's math
+        dma_tile(nx.k, nx.kd, tid);
+        dma_tile(nx.v, nx.vd, tid);
+      }
+      if ((f >> item) & 1) full_block<B>(tables, ws, scale);
+    };
+    for (; u < n_full; u += 2) {  // unrolled by two: each block's buffer is a constant
+      run_full(u, std::integral_constant<int, 0>{});
+      if (u + 1 < n_full) run_full(u + 1, std::integral_constant<int, 1>{});
+    }
+    u = n_full;
+    for (; u < nu; ++u) {
+      const int cur = u & 1;
+      const int j = __builtin_amdgcn_readfirstlane(ulist[u]);
+      const int f = __builtin_amdgcn_readfirstlane(uflag[u]);
+      begin_block(u);
+      if ((f >> item) & 1) {
+        if (j != t) {
+          exact_block<4, false>(kbuf[cur], vbuf[cur], ws, scale, q_pos);
+        } else {
+          switch (wi) {  // wave wi reaches key sub-blocks 0 .. wi of the diagonal block
+            case 0: exact_block<1, true>(kbuf[cur], vbuf[cur], ws, scale, q_pos); break;
+            case 1: exact_block<2, true>(kbuf[cur], vbuf[cur], ws, scale, q_pos); break;
+            case 2: exact_block<3, true>(kbuf[cur], vbuf[cur], ws, scale, q_pos); break;
+            default: exact_block<4, true>(kbuf[cur], vbuf[cur], ws, scale, q_pos); break;
+          }
         }
       }
-      __syncthreads();  // every wave is done with the tile before it is refilled
     }
+    __syncthreads();  // every wave is done with the last block
   }
 
   if (TAIL) {
-    // bitmap of listed blocks, then {j < t : not listed} ascending into blist
-    if (tid < kMaxBlocksAttn / 32) listed[tid] = 0u;
-    __syncthreads();
-    for (int i = tid; i < n; i += kAttnThreads) {
-      const int j = blist[i];
-      atomicOr(&listed[j >> 5], 1u << (j & 31));
-    }
-    __syncthreads();
-    int ntail = 0;
-    for (int j0 = 0; j0 < t; j0 += kAttnThreads) {
-      const int j = j0 + tid;
-      const bool in_tail = j < t && ((listed[j >> 5] >> (j & 31)) & 1u) == 0u;
-      ntail = compact_append(in_tail, j, blist, ntail, wave_counts);
+    // tail of item i: {j < t_i : not listed for i}, ascending. Both items' tails
+    // are staged side by side (item i uses buffer i) and processed together.
+    __shared__ int16_t tlist[2][kMaxBlocksAttn];
+    int ntail[2] = {0, 0};
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int tt = t_item[it];
+      for (int j0 = 0; j0 < max(tt, 0); j0 += kAttnThreads) {
+        const int j = j0 + tid;
+        const bool in_tail = j < tt && ((bits[it][j >> 5] >> (j & 31)) & 1u) == 0u;
+        const uint64_t ballot = __ballot(in_tail);
+        const int before = __popcll(ballot & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_counts[w] = __popcll(ballot);
+        __syncthreads();
+        int offset = ntail[it];
+        for (int x = 0; x < w; ++x) offset += wave_counts[x];
+        if (in_tail) tlist[it][offset + before] = (int16_t)j;
+        for (int x = 0; x < kAttnThreads / 64; ++x) ntail[it] += wave_counts[x];
+        __syncthreads();
+      }
     }
     const int64_t desc_base = (int64_t)b * a.blocks * a.kv_heads + g;  // (b, 0, g)
-    for (int t0 = 0; t0 < ntail; t0 += kTailTile) {
+    const int nmax = max(ntail[0], ntail[1]);
+    for (int t0 = 0; t0 < nmax; t0 += kTailTile) {
       __syncthreads();
-      // K rows i (hi) and 64 + i (lo) of mean K; value slots 0..63 of mean V
-      for (int e = tid; e < kTailTile * kHeadDim; e += kAttnThreads) {
-        const int i = e >> 7, d = e & 127;
-        const int j = (t0 + i < ntail) ? (int)blist[t0 + i] : -1;
-        float mk = 0.0f, mv = 0.0f;
-        if (j >= 0) {
-          const int64_t off = (desc_base + (int64_t)j * a.kv_heads) * kHeadDim + d;
-          mk = a.mean_k[off];
-          mv = a.mean_v[off];
-        }
-        const uint16_t hi = to_bf16_bits(mk);
-        const uint16_t lo = to_bf16_bits(mk - __uint_as_float((uint32_t)hi << 16));
-        kbuf[swz(i, d >> 3) + (d & 7)] = hi;
-        kbuf[swz(kTailTile + i, d >> 3) + (d & 7)] = lo;
-        const int slot = value_slot_of_key(i);
-        vbuf[swz(d, slot >> 3) + (slot & 7)] = to_bf16_bits(mv);
-        if (d == 0) tail_bias[i] = j >= 0 ? logf((float)a.bcounts[j]) * kLog2e : -INFINITY;
+      stage_tail(a, tlist[item], ntail[item], t0, desc_base, kbuf[item], vbuf[item], tail_bias[item],
+                 tid & (kItemWaves * 64 - 1), kItemWaves * 64);
+      __syncthreads();
+      if (t0 < ntail[item]) {
+        f32x16 s[4];
+        bf16x8 pb[8];
+        scores<2, true>(kbuf[item], ws, 0, s);
+        softmax<2, false, true>(s, ws, scale, q_pos, tail_bias[item], 0, pb);
+        accumulate_pv<4>(vbuf[item], ws, pb);
       }
-      __syncthreads();
-      f32x16 s[4];
-      bf16x8 pb[8];
-      scores<2, true>(kbuf, ws, 0, s);
-      softmax<2, false, true>(s, ws, scale, q_pos, tail_bias, 0, pb);
-      accumulate_pv<4>(vbuf, ws, pb);
     }
   }
 
@@ -399,7 +697,7 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_kernel(AttnArgs a) {
   const bool any = l > 0.0f;
   const float inv = any ? 1.0f / l : 0.0f;
   const int64_t qrow = (int64_t)t * kBlock + q_pos;
-  if (qrow < a.seq) {
+  if (live && qrow < a.seq) {
     if (OUT_F32) {
       float* dst = static_cast<float*>(a.out) + b * a.os_b + qrow * a.os_s + h * a.os_h;
 #pragma unroll
@@ -556,7 +854,7 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
   if (lse) { a.ls_b = lse_strides[0]; a.ls_s = lse_strides[1]; a.ls_h = lse_strides[2]; }
   a.batch = batch; a.seq = seq; a.q_heads = q_heads; a.kv_heads = kv_heads;
   a.blocks = blocks; a.group = q_heads / kv_heads;
-  a.num_pairs = blocks * batch * kv_heads;
+  a.num_pairs = ((blocks + 1) / 2) * batch * kv_heads;  // (tile pair, batch, kv group)
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
   const int grid = ((a.num_pairs + 7) / 8) * 8 * a.group;
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -8,7 +8,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/sparse_prefill.h"
+#include "sparse_prefill.h"
 
 namespace spx {
 
