@@ -12,7 +12,10 @@ resident in HBM. ``value`` = ms per layer (lower is better).
 Also reported on the same line:
   roofline      the attention kernel's algorithmic FLOP rate (8,388,608 x selected
                 128x128 tiles / its HIP-event duration inside the timed region)
-                against the 2.5 PFLOP/s bf16 dense MFMA peak;
+                against the 2.5 PFLOP/s bf16 dense MFMA peak, plus its HBM bytes per
+                launch (profiles/hbm_traffic.json, from rocprofv3 FETCH/WRITE_SIZE);
+  achievable    measured ceilings on the same box: an 8192^3 bf16 GEMM (hipBLASLt
+                through torch) and a 1 GiB device copy;
   methods       ms/layer and selected-block density of all six methods;
   stages        per-stage kernel times with their roofline fractions;
   cpu_baseline  the CPU oracle (numpy restatement of the reference path) on a
@@ -105,6 +108,33 @@ def stage_profile(backend, q, k, v, scale, torch):
     for name in ("descriptor", "selector", "indices", "exact"):
         out[name] = sorted(r[f"{name}_ms"] for r in rows)[len(rows) // 2]
     return out
+
+
+def achievable_peaks(torch):
+    """Measured ceilings on this box: a large bf16 GEMM through torch (hipBLASLt)
+    and a device-to-device copy, for context next to the nominal peaks."""
+    a = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+    for _ in range(3):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    reps = 20
+    for _ in range(reps):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    gemm = 2 * 8192 ** 3 * reps / (time.perf_counter() - t0) / 1e12
+    del a, b
+    x = torch.empty(1 << 29, device="cuda", dtype=torch.bfloat16)   # 1 GiB
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    copy = 2 * x.numel() * 2 * 10 / (time.perf_counter() - t0) / 1e9
+    return {"gemm_bf16_8192_tflops": round(gemm, 1), "copy_1gib_gbs": round(copy, 1)}
 
 
 def cpu_baseline(q, k, v, scale, method, alpha, sample_tiles, budget_s):
@@ -240,6 +270,8 @@ def main():
         methods["dense_hip"] = {"ms_per_layer": round(timed_forward(b, qg, kg, vg, scale, 5, 2, torch), 3),
                                 "block_density": 1.0}
 
+    achievable = achievable_peaks(torch)
+
     baseline = None
     if not args.no_cpu_baseline:
         baseline = cpu_baseline(q, k, v, scale, args.method, args.alpha, args.cpu_sample_tiles,
@@ -277,7 +309,9 @@ def main():
             "kernel_ms": round(kernel_ms, 4),
             "selected_tiles": n_sel,
             "flops_per_launch": flops,
+            "frac_of_achievable_gemm": round(achieved / achievable["gemm_bf16_8192_tflops"], 4),
         },
+        "achievable": achievable,
         "effective_tflops": round(4 * head_dim * exact_pairs / (ms * 1e-3) / 1e12, 1),
         "block_density": round(density, 5),
         "stages": stage_report,

@@ -1,0 +1,183 @@
+"""Measurement runs beyond the headline bench line (one GPU, synthetic data).
+
+  python -m exp3_amd.sweeps needles [--seq 32640] [--needles 64]
+      planted-retrieval inputs; alpha in {0.04, 0.08, 0.16} for the four mean
+      methods, fp_v1 at 0.08 and dense: ms/layer, selected-block density
+      counts.sum() / (H NB (NB + 1) / 2) and the exact-pair ratio
+      (kernels.py:338-353 accounting)
+  python -m exp3_amd.sweeps long [--seq 131072] [--needles 256]
+      long context: cgf_mean and dispersion_mean at alpha 0.04 (plus mean_native
+      at 0.04 for reference), same columns
+  python -m exp3_amd.sweeps model [--seq 32640] [--layers 28] [--repeats 3]
+      full prefill of a random-init Qwen2.5-7B-shaped model built from a local
+      config (28 layers, hidden 3584, FFN 18944, 28/4 heads, RMSNorm 1e-6,
+      theta 1e6, vocab 152064, QKV bias, bf16) with the attention backend
+      registered as transformers' "sdpa" function. Timing follows
+      evaluate.py:323-345: ids already on the GPU, sync, timer, model(ids,
+      use_cache=True, logits_to_keep=1), argmax, sync; each method warmed up
+      first (evaluate.py:634-644), repeats with rotated method order
+      (evaluate.py:646-663), median reported (report.py:33-42); then 128 greedy
+      dense decode tokens (not timed) to exercise the decode path.
+
+Every run prints one JSON object per measured case.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import sys
+import time
+
+MEAN_FOUR = ("mean_native", "mean_balanced", "cgf_mean", "dispersion_mean")
+
+
+class _Layer:
+    layer_idx = 0
+
+
+def _layer_case(torch, attention, kernels, q, k, v, method, alpha, steps=5, warmup=2):
+    scale = q.shape[-1] ** -0.5
+    backend = attention.AttentionBackend(alpha=alpha, register=False)
+    backend.configure(method, alpha)
+    qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    for _ in range(warmup):
+        backend.forward(_Layer(), qt, kt, vt, None, scale)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        backend.forward(_Layer(), qt, kt, vt, None, scale)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1000.0 / steps
+    seq, heads = q.shape[1], q.shape[2]
+    blocks = math.ceil(seq / 128)
+    if method == "dense":
+        density, pair_ratio = 1.0, 1.0
+    else:
+        record = {"events": {}}
+        if method in attention.V1_ROUTED_METHODS:
+            _, _, cnt, sel = backend._v1_selection(q, k, scale, record, v)
+        else:
+            _, _, _, cnt, sel = backend._new_selection(q, k, v, scale, record)
+        acct = kernels.selection_accounting(sel, seq, 128, 128, method, 32)
+        density = float(cnt.sum().item()) / (heads * blocks * (blocks + 1) / 2)
+        pair_ratio = float(acct["effective_exact_token_pair_ratio"].item())
+    return {"method": method, "alpha": alpha if method != "dense" else None, "seq": seq,
+            "ms_per_layer": round(ms, 3), "block_density": round(density, 5),
+            "exact_pair_ratio": round(pair_ratio, 5)}
+
+
+def run_layer_sweep(seq, needles, seed, cases, label):
+    import torch
+    from exp3_amd import _lib, attention, kernels, synthetic
+    _lib.load()
+    q, k, v, positions = synthetic.make_inputs(seq, seed=seed, needles=needles, device="cuda")
+    for method, alpha in cases:
+        row = _layer_case(torch, attention, kernels, q, k, v, method, alpha)
+        row.update({"sweep": label, "needles": needles, "seed": seed})
+        print(json.dumps(row), flush=True)
+
+
+def qwen2_7b_config(layers):
+    from transformers import Qwen2Config
+    return Qwen2Config(vocab_size=152064, hidden_size=3584, intermediate_size=18944,
+                       num_hidden_layers=layers, num_attention_heads=28, num_key_value_heads=4,
+                       rms_norm_eps=1e-6, rope_theta=1e6, max_position_embeddings=32768,
+                       tie_word_embeddings=False, use_sliding_window=False,
+                       attn_implementation="sdpa", torch_dtype="bfloat16")
+
+
+def run_model(seq, layers, repeats, seed, methods, alpha, decode_tokens):
+    import torch
+    from transformers import Qwen2ForCausalLM
+    from exp3_amd import _lib, attention
+    _lib.load()
+    backend = attention.AttentionBackend(alpha=alpha)   # registers as transformers' "sdpa"
+    cfg = qwen2_7b_config(layers)
+    torch.manual_seed(seed)
+    torch.set_default_dtype(torch.bfloat16)
+    with torch.device("cuda"):
+        model = Qwen2ForCausalLM(cfg)
+    torch.set_default_dtype(torch.float32)
+    model.eval()
+    params = sum(p.numel() for p in model.parameters())
+    gen = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, cfg.vocab_size, (1, seq), generator=gen).to("cuda")
+
+    def prefill(method):
+        backend.configure(method, alpha)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            out = model(ids, use_cache=True, logits_to_keep=1)
+            token = out.logits[:, -1].argmax(-1)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1000.0, out, token
+
+    for m in methods:                        # warm-up, one prefill per method
+        prefill(m)
+    times = {m: [] for m in methods}
+    for r in range(repeats):                 # rotated method order
+        order = methods[r % len(methods):] + methods[:r % len(methods)]
+        for m in order:
+            ms, _, _ = prefill(m)
+            times[m].append(ms)
+    dense_ms = sorted(times["dense"])[len(times["dense"]) // 2] if "dense" in times else None
+    for m in methods:
+        med = sorted(times[m])[len(times[m]) // 2]
+        print(json.dumps({"sweep": "model", "method": m, "alpha": alpha if m != "dense" else None,
+                          "seq": seq, "layers": layers, "params": params,
+                          "prefill_ms_median": round(med, 1),
+                          "prefill_ms_all": [round(x, 1) for x in times[m]],
+                          "speedup_vs_dense": round(dense_ms / med, 3) if dense_ms else None}),
+              flush=True)
+    # greedy dense decode (not timed): exercises the backend's decode branch
+    _, out, token = prefill("dense")
+    cache = out.past_key_values
+    generated = [int(token.item())]
+    with torch.no_grad():
+        for _ in range(decode_tokens):
+            step = model(token[:, None], past_key_values=cache, use_cache=True, logits_to_keep=1)
+            cache = step.past_key_values
+            token = step.logits[:, -1].argmax(-1)
+            generated.append(int(token.item()))
+    print(json.dumps({"sweep": "model-decode", "tokens": decode_tokens,
+                      "cache_len": seq + decode_tokens, "first_ids": generated[:8]}), flush=True)
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description="measurement sweeps (one GPU)")
+    sub = p.add_subparsers(dest="cmd", required=True)
+    n = sub.add_parser("needles")
+    n.add_argument("--seq", type=int, default=32640)
+    n.add_argument("--needles", type=int, default=64)
+    n.add_argument("--seed", type=int, default=17)
+    lo = sub.add_parser("long")
+    lo.add_argument("--seq", type=int, default=131072)
+    lo.add_argument("--needles", type=int, default=256)
+    lo.add_argument("--seed", type=int, default=17)
+    mo = sub.add_parser("model")
+    mo.add_argument("--seq", type=int, default=32640)
+    mo.add_argument("--layers", type=int, default=28)
+    mo.add_argument("--repeats", type=int, default=3)
+    mo.add_argument("--seed", type=int, default=17)
+    mo.add_argument("--alpha", type=float, default=0.08)
+    mo.add_argument("--decode-tokens", type=int, default=128)
+    mo.add_argument("--methods", default="dense,fp_v1,mean_native,mean_balanced,cgf_mean,dispersion_mean")
+    args = p.parse_args(argv)
+    if args.cmd == "needles":
+        cases = [(m, a) for a in (0.04, 0.08, 0.16) for m in MEAN_FOUR]
+        cases += [("fp_v1", 0.08), ("dense", 0.08)]
+        run_layer_sweep(args.seq, args.needles, args.seed, cases, "needles")
+    elif args.cmd == "long":
+        cases = [("cgf_mean", 0.04), ("dispersion_mean", 0.04), ("mean_native", 0.04)]
+        run_layer_sweep(args.seq, args.needles, args.seed, cases, "long")
+    else:
+        run_model(args.seq, args.layers, args.repeats, args.seed, args.methods.split(","),
+                  args.alpha, args.decode_tokens)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
