@@ -203,7 +203,11 @@ class AttentionBackend:
 
     # --------------------------------------------------------- attention
 
-    def _attention(self, q, k, tiles, indices, counts, scale, descriptors: BlockDescriptors | None):
+    def _attention(self, q, k, tiles, indices, counts, scale, descriptors: BlockDescriptors | None,
+                   rescue=None):
+        """One attention-kernel launch: exact blocks, plus the block-mean tail
+        (``descriptors``) or the rescue tail (``rescue`` = (choice, remainder,
+        descriptors-or-None)) in the same online softmax."""
         device = q.device
         batch, sequence, q_heads, head_dim = q.shape
         output = torch.empty(batch, sequence, q_heads, head_dim, dtype=q.dtype, device=device)
@@ -218,7 +222,12 @@ class AttentionBackend:
         if self.kernel_events is not None:
             events = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             events[0].record()
-        if descriptors is None:
+        if rescue is not None:
+            choice, remainder, rdesc = rescue
+            _lib.call("spx_sparse_attention_rescue", *common_head, _lib.ptr(choice),
+                      _lib.ptr(rdesc.mean_k if rdesc else None),
+                      _lib.ptr(rdesc.mean_v if rdesc else None), int(remainder), *common_tail)
+        elif descriptors is None:
             _lib.call("spx_exact_attention", *common_head, *common_tail)
         else:
             _lib.call("spx_sparse_attention_mean", *common_head, _lib.ptr(descriptors.mean_k),
@@ -273,9 +282,6 @@ class AttentionBackend:
             if self.record:
                 record["accounting"] = self._dense_accounting(query)
         else:
-            if self.method in RESCUE_METHODS:
-                raise NotImplementedError(
-                    f"method {self.method!r} (rescue tail) is not built for MI355X")
             _lib.require_gpu(query, key, value)
             q = _lib.kernel_view(query.transpose(1, 2))
             k = _lib.kernel_view(key.transpose(1, 2))
@@ -284,7 +290,8 @@ class AttentionBackend:
             capture_v1 = self.capture_callback is not None and self.method == "fp_v1"
             if self.method in V1_ROUTED_METHODS:
                 kbar, descriptors, tiles, scores, indices, counts, selected = self._route_v1(
-                    q, k, v, scale, record, self.method == "mean_native", True,
+                    q, k, v, scale, record,
+                    self.method in ("mean_native", "fp_v1_rescue_v2"), True,
                     want_scores=capture_v1)
             else:
                 descriptors, tiles, indices, counts, selected = self._new_selection(
@@ -297,9 +304,18 @@ class AttentionBackend:
                     indices=indices, counts=counts, selected=selected, scale=scale)
 
             mean_desc = descriptors if self.method in MEAN_METHODS else None
+            rescue = None
+            if self.method in RESCUE_METHODS:
+                # the rescue-token choice is timed as the "mean" stage (the non-exact
+                # tail path of the profile schema, attention.py:306-307); the tail
+                # itself runs inside the attention kernel
+                choice = self._stage(
+                    record, "mean",
+                    lambda: kernels.rescue_choice(q, tiles[0], self.block_size))
+                rescue = (choice, self.method == "fp_v1_rescue_v2", descriptors)
             output, _ = self._stage(
                 record, "exact",
-                lambda: self._attention(q, k, tiles, indices, counts, scale, mean_desc))
+                lambda: self._attention(q, k, tiles, indices, counts, scale, mean_desc, rescue))
             if self.record:
                 q_tile, k_tile = upstream.attention_tile_sizes()
                 score_tile = upstream.score_tile_size() if self.method in V1_ROUTED_METHODS else None

@@ -59,6 +59,8 @@ struct AttnArgs {
   const float* mean_k;  // [B, NB, Hkv, D]
   const float* mean_v;
   const int32_t* bcounts;  // [NB]
+  const uint8_t* choice;   // rescue token per (b, t, j, h): [B, NB, NB, Hq]
+  int tail_kind;           // 0 block means, 1 rescue token, 2 rescue token + remainder mean
   void* out;
   int64_t os_b, os_s, os_h;
   float* lse;  // nullable
@@ -69,6 +71,11 @@ struct AttnArgs {
 
 __device__ __forceinline__ int swz(int row, int chunk) {
   return row * kBlock + ((chunk ^ (row & 15)) << 3);
+}
+
+// In-row offset of element c of row `row` in a swizzled tile.
+__device__ __forceinline__ int swz_off(int row, int c) {
+  return (((c >> 3) ^ (row & 15)) << 3) + (c & 7);
 }
 
 __device__ __forceinline__ bf16x8 lds_read16(const uint16_t* lds, int off) {
@@ -477,6 +484,50 @@ __device__ __forceinline__ void stage_tail(const AttnArgs& a, const int16_t* ids
   }
 }
 
+// Rescue tail tile (kernels.py:233-309): entries per block epb = 1 (the block's
+// rescue token: its key row, its value, logit bias 0) or 2 (also the mean of the
+// other 127 tokens: (mean * 128 - token) / 127 for key and value, bias ln 127
+// log2 e). Blocks t0 .. t0 + kTailTile / epb - 1 of `ids`; K rows as in
+// stage_tail (hi row i, lo row 64 + i), values in slots 0..63. The token's key and
+// value come from the pool pass's key / value tiles of block j.
+__device__ __forceinline__ void stage_rescue(const AttnArgs& a, const int16_t* ids, int ntail,
+                                             int t0, int epb, int b, int g, int h, int t,
+                                             uint16_t* kb, uint16_t* vb, float* bias, int tid0,
+                                             int stride) {
+  const int64_t tile_elems = (int64_t)kBlock * kHeadDim;
+  for (int e = tid0; e < kTailTile * kHeadDim; e += stride) {
+    const int i = e >> 7, d = e & 127;
+    const int blk = t0 + i / epb, kind = i % epb;
+    const int j = blk < ntail ? (int)ids[blk] : -1;
+    float mk = 0.0f, mv = 0.0f, bi = -INFINITY;
+    if (j >= 0) {
+      const int tok = a.choice[(((int64_t)b * a.blocks + t) * a.blocks + j) * a.q_heads + h];
+      const int64_t tile = (((int64_t)b * a.kv_heads + g) * a.blocks + j) * tile_elems;
+      const float kval =
+          __uint_as_float((uint32_t)a.kt[tile + tok * kHeadDim + swz_off(tok, d)] << 16);
+      const int slot = value_slot_of_key(tok);
+      const float vval = __uint_as_float((uint32_t)a.vt[tile + d * kBlock + swz_off(d, slot)] << 16);
+      if (kind == 0) {
+        mk = kval;
+        mv = vval;
+        bi = 0.0f;
+      } else {
+        const int64_t off = (((int64_t)b * a.blocks + j) * a.kv_heads + g) * kHeadDim + d;
+        mk = (a.mean_k[off] * (float)kBlock - kval) / (float)(kBlock - 1);
+        mv = (a.mean_v[off] * (float)kBlock - vval) / (float)(kBlock - 1);
+        bi = logf((float)(kBlock - 1)) * kLog2e;
+      }
+    }
+    const uint16_t hi = to_bf16_bits(mk);
+    const uint16_t lo = to_bf16_bits(mk - __uint_as_float((uint32_t)hi << 16));
+    kb[swz(i, d >> 3) + (d & 7)] = hi;
+    kb[swz(kTailTile + i, d >> 3) + (d & 7)] = lo;
+    const int vslot = value_slot_of_key(i);
+    vb[swz(d, vslot >> 3) + (vslot & 7)] = to_bf16_bits(mv);
+    if (d == 0) bias[i] = bi;
+  }
+}
+
 template <bool EXACT, bool TAIL, bool OUT_F32>
 __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
   // ---- work item: query tiles (t, t - 1) of one q head. Tile pairs heaviest first,
@@ -677,10 +728,15 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
     }
     const int64_t desc_base = (int64_t)b * a.blocks * a.kv_heads + g;  // (b, 0, g)
     const int nmax = max(ntail[0], ntail[1]);
-    for (int t0 = 0; t0 < nmax; t0 += kTailTile) {
+    const int epb = a.tail_kind == 2 ? 2 : 1;   // tail entries per unselected block
+    for (int t0 = 0; t0 < nmax; t0 += kTailTile / epb) {
       __syncthreads();
-      stage_tail(a, tlist[item], ntail[item], t0, desc_base, kbuf[item], vbuf[item], tail_bias[item],
-                 tid & (kItemWaves * 64 - 1), kItemWaves * 64);
+      if (a.tail_kind == 0)
+        stage_tail(a, tlist[item], ntail[item], t0, desc_base, kbuf[item], vbuf[item],
+                   tail_bias[item], tid & (kItemWaves * 64 - 1), kItemWaves * 64);
+      else
+        stage_rescue(a, tlist[item], ntail[item], t0, epb, b, g, h, t, kbuf[item], vbuf[item],
+                     tail_bias[item], tid & (kItemWaves * 64 - 1), kItemWaves * 64);
       __syncthreads();
       if (t0 < ntail[item]) {
         f32x16 s[4];
@@ -795,6 +851,8 @@ namespace {
 
 struct AttnRequest {
   bool exact, tail, out_f32;
+  int tail_kind;             // 0 block means, 1 rescue token, 2 rescue token + remainder
+  const uint8_t* choice;     // rescue tokens (tail_kind > 0)
 };
 
 int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_strides,
@@ -823,9 +881,17 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
     SPX_REQUIRE(value_tiles != nullptr && (reinterpret_cast<uintptr_t>(value_tiles) & 15) == 0,
                 SPX_EINVAL, "value_tiles: null or not 16-byte aligned");
   }
-  if (req.tail) {
+  if (req.tail && req.tail_kind == 0) {
     SPX_REQUIRE(mean_k && mean_v && block_counts, SPX_EINVAL,
                 "mean correction needs mean_k, mean_v and block_counts");
+  }
+  if (req.tail && req.tail_kind > 0) {
+    SPX_REQUIRE(req.choice != nullptr, SPX_EINVAL, "rescue tail needs the rescue token choice");
+    SPX_REQUIRE(key_tiles != nullptr && (reinterpret_cast<uintptr_t>(key_tiles) & 15) == 0 &&
+                    value_tiles != nullptr && (reinterpret_cast<uintptr_t>(value_tiles) & 15) == 0,
+                SPX_EINVAL, "rescue tail needs 16-byte aligned key_tiles and value_tiles");
+    SPX_REQUIRE(req.tail_kind == 1 || (mean_k && mean_v), SPX_EINVAL,
+                "rescue remainder needs mean_k and mean_v");
   }
   if (indices) {
     SPX_REQUIRE(index_strides && counts && count_strides, SPX_EINVAL,
@@ -848,6 +914,7 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
     a.cs_b = count_strides[0]; a.cs_t = count_strides[1]; a.cs_h = count_strides[2];
   }
   a.mean_k = mean_k; a.mean_v = mean_v; a.bcounts = block_counts;
+  a.choice = req.choice; a.tail_kind = req.tail ? req.tail_kind : 0;
   a.out = out;
   a.os_b = out_strides[0]; a.os_s = out_strides[1]; a.os_h = out_strides[2];
   a.lse = lse;
@@ -874,7 +941,7 @@ extern "C" int spx_exact_attention(const void* q, const int64_t* q_strides,
                                    int block_size, float scale, void* out,
                                    const int64_t* out_strides, float* lse,
                                    const int64_t* lse_strides, void* stream) {
-  return launch_attention({true, false, false}, q, q_strides, key_tiles, value_tiles, indices,
+  return launch_attention({true, false, false, 0, nullptr}, q, q_strides, key_tiles, value_tiles, indices,
                           index_strides, counts, count_strides, nullptr, nullptr, nullptr, batch,
                           seq, q_heads, kv_heads, head_dim, block_size, scale, out, out_strides,
                           lse, lse_strides, stream);
@@ -889,7 +956,7 @@ extern "C" int spx_sparse_attention_mean(const void* q, const int64_t* q_strides
                                          int q_heads, int kv_heads, int head_dim, int block_size,
                                          float scale, void* out, const int64_t* out_strides,
                                          float* lse, const int64_t* lse_strides, void* stream) {
-  return launch_attention({true, true, false}, q, q_strides, key_tiles, value_tiles, indices,
+  return launch_attention({true, true, false, 0, nullptr}, q, q_strides, key_tiles, value_tiles, indices,
                           index_strides, counts, count_strides, mean_k, mean_v, block_counts,
                           batch, seq, q_heads, kv_heads, head_dim, block_size, scale, out,
                           out_strides, lse, lse_strides, stream);
@@ -903,7 +970,7 @@ extern "C" int spx_mean_tail(const void* q, const int64_t* q_strides, const int6
                              float* out, const int64_t* out_strides, float* lse,
                              const int64_t* lse_strides, void* stream) {
   SPX_REQUIRE(indices != nullptr, SPX_EINVAL, "mean_tail: indices must be given");
-  return launch_attention({false, true, true}, q, q_strides, nullptr, nullptr, indices,
+  return launch_attention({false, true, true, 0, nullptr}, q, q_strides, nullptr, nullptr, indices,
                           index_strides, counts, count_strides, mean_k, mean_v, block_counts,
                           batch, seq, q_heads, kv_heads, head_dim, block_size, scale, out,
                           out_strides, lse, lse_strides, stream);
@@ -951,3 +1018,32 @@ extern "C" int spx_merge_exact_mean(const void* exact_out, const int64_t* exact_
   merge_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   return launch_status("merge_exact_mean");
 }
+
+extern "C" int spx_sparse_attention_rescue(
+    const void* q, const int64_t* q_strides, const void* key_tiles, const void* value_tiles,
+    const int64_t* indices, const int64_t* index_strides, const int32_t* counts,
+    const int64_t* count_strides, const uint8_t* choice, const float* mean_k, const float* mean_v,
+    int remainder, int batch, int seq, int q_heads, int kv_heads, int head_dim, int block_size,
+    float scale, void* out, const int64_t* out_strides, float* lse, const int64_t* lse_strides,
+    void* stream) {
+  return launch_attention({true, true, false, remainder ? 2 : 1, choice}, q, q_strides, key_tiles,
+                          value_tiles, indices, index_strides, counts, count_strides, mean_k,
+                          mean_v, nullptr, batch, seq, q_heads, kv_heads, head_dim, block_size,
+                          scale, out, out_strides, lse, lse_strides, stream);
+}
+
+extern "C" int spx_rescue_tail(const void* q, const int64_t* q_strides, const void* key_tiles,
+                               const void* value_tiles, const int64_t* indices,
+                               const int64_t* index_strides, const int32_t* counts,
+                               const int64_t* count_strides, const uint8_t* choice,
+                               const float* mean_k, const float* mean_v, int remainder, int batch,
+                               int seq, int q_heads, int kv_heads, int head_dim, int block_size,
+                               float scale, float* out, const int64_t* out_strides, float* lse,
+                               const int64_t* lse_strides, void* stream) {
+  SPX_REQUIRE(indices != nullptr, SPX_EINVAL, "rescue_tail: indices must be given");
+  return launch_attention({false, true, true, remainder ? 2 : 1, choice}, q, q_strides, key_tiles,
+                          value_tiles, indices, index_strides, counts, count_strides, mean_k,
+                          mean_v, nullptr, batch, seq, q_heads, kv_heads, head_dim, block_size,
+                          scale, out, out_strides, lse, lse_strides, stream);
+}
+

@@ -175,9 +175,73 @@ def mean_tail(q: torch.Tensor, descriptors: BlockDescriptors, selected: torch.Te
     return output, lse
 
 
-def rescue_tail(*args, **kwargs):
-    """kernels.py:233-309 is not part of this MI355X path (rescue methods)."""
-    raise NotImplementedError("rescue_tail (fp_v1_rescue / fp_v1_rescue_v2) is not built for MI355X")
+def _pool_tiles_and_means(k: torch.Tensor, v: torch.Tensor, block_size: int):
+    """One spx_block_pool launch -> (key tiles, value tiles, fp32 mean K, fp32 mean V)."""
+    device = _lib.require_gpu(k, v)
+    k = _lib.kernel_view(k)
+    v = _lib.kernel_view(v)
+    batch, sequence, kv_heads, head_dim = k.shape
+    blocks = _blocks(sequence, block_size)
+    key_tiles = torch.empty(batch, kv_heads, blocks, block_size, head_dim, dtype=torch.bfloat16,
+                            device=device)
+    value_tiles = torch.empty(batch, kv_heads, blocks, head_dim, block_size, dtype=torch.bfloat16,
+                              device=device)
+    mean_k = torch.empty(batch, blocks, kv_heads, head_dim, dtype=torch.float32, device=device)
+    mean_v = torch.empty_like(mean_k)
+    _lib.call("spx_block_pool", _lib.ptr(k), _lib.strides(k), _lib.ptr(v), _lib.strides(v), batch,
+              sequence, kv_heads, head_dim, block_size, None, _lib.ptr(mean_k), _lib.ptr(mean_v),
+              None, None, None, _lib.ptr(key_tiles), _lib.ptr(value_tiles), _lib.stream(device))
+    return key_tiles, value_tiles, mean_k, mean_v
+
+
+def rescue_choice(q: torch.Tensor, key_tiles: torch.Tensor, block_size: int = BLOCK_SIZE):
+    """Rescue token of every (query tile t, key block j < t, q head): argmax over the
+    block's positions of the tile's mean query . k (kernels.py:274-283), uint8
+    ``[B, NB, NB, Hq]`` (0 where j >= t). ``key_tiles`` from the pooling pass."""
+    device = _lib.require_gpu(q, key_tiles)
+    q = _lib.kernel_view(q)
+    batch, sequence, q_heads, head_dim = q.shape
+    kv_heads = key_tiles.shape[1]
+    blocks = _blocks(sequence, block_size)
+    qmean = torch.empty(batch, blocks, q_heads, head_dim, dtype=torch.float32, device=device)
+    choice = torch.empty(batch, blocks, blocks, q_heads, dtype=torch.uint8, device=device)
+    _lib.call("spx_tile_mean_query", _lib.ptr(q), _lib.strides(q), batch, sequence, q_heads,
+              head_dim, block_size, _lib.ptr(qmean), _lib.stream(device))
+    _lib.call("spx_rescue_choice", _lib.ptr(qmean), _lib.ptr(key_tiles.contiguous()), batch,
+              sequence, q_heads, kv_heads, head_dim, block_size, _lib.ptr(choice),
+              _lib.stream(device))
+    return choice
+
+
+@torch.no_grad()
+def rescue_tail(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, selected: torch.Tensor,
+                scale: float, block_size: int = BLOCK_SIZE, chunk_tiles: int = 8,
+                remainder: bool = False):
+    """Exact attention to one rescue token per unselected full-history block in
+    FP32 -> (output, natural-log LSE) (kernels.py:233-309). Per query tile t and head
+    h, the rescue token of block j is argmax_p qbar_{t,h} . k_{j,p}; with
+    ``remainder`` the other B-1 tokens of the block also enter through their mean
+    K / V with multiplicity B-1. ``chunk_tiles`` is accepted for interface parity
+    (the kernel processes every tile in one launch)."""
+    device = _lib.require_gpu(q, k, v, selected)
+    q = _lib.kernel_view(q)
+    batch, sequence, q_heads, head_dim = q.shape
+    blocks = _blocks(sequence, block_size)
+    if tuple(selected.shape) != (batch, blocks, blocks, q_heads):
+        raise ValueError(f"selected shape {tuple(selected.shape)}, expected "
+                         f"{(batch, blocks, blocks, q_heads)}")
+    key_tiles, value_tiles, mean_k, mean_v = _pool_tiles_and_means(k, v, block_size)
+    choice = rescue_choice(q, key_tiles, block_size)
+    indices, counts = indices_from_mask(selected)
+    output = torch.empty(batch, sequence, q_heads, head_dim, dtype=torch.float32, device=device)
+    lse = torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
+    _lib.call("spx_rescue_tail", _lib.ptr(q), _lib.strides(q), _lib.ptr(key_tiles),
+              _lib.ptr(value_tiles), _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
+              _lib.strides(counts), _lib.ptr(choice), _lib.ptr(mean_k), _lib.ptr(mean_v),
+              int(bool(remainder)), batch, sequence, q_heads, k.shape[2], head_dim, block_size,
+              float(scale), _lib.ptr(output), _lib.strides(output), _lib.ptr(lse),
+              _lib.strides(lse), _lib.stream(device))
+    return output, lse
 
 
 @torch.no_grad()

@@ -37,7 +37,7 @@ extern "C" {
 #define SPX_EUNSUPPORTED (-2) /* valid in the reference, not built here       */
 #define SPX_ELAUNCH (-3)      /* HIP launch / runtime failure                 */
 
-#define SPX_ABI_VERSION 2
+#define SPX_ABI_VERSION 3
 
 /* Selector ids for spx_selector_scores (kernels.py:62). */
 #define SPX_SELECTOR_MEAN_BALANCED 0
@@ -203,6 +203,50 @@ int spx_merge_exact_mean(const void* exact_out, const int64_t* exact_strides,
                          int seq, int heads, int head_dim, void* out,
                          const int64_t* out_strides, float* lse_out,
                          const int64_t* lse_out_strides, void* stream);
+
+/* ---------------------------------------------------------- rescue tail */
+
+/* Mean query of every query tile over its real rows: fp32 [B, NB, Hq, D]
+ * (contiguous, caller-allocated). Replaces the q_mean of kernels.py:274-276
+ * (rescue_tail). */
+int spx_tile_mean_query(const void* q, const int64_t* q_strides, int batch, int seq, int q_heads,
+                        int head_dim, int block_size, float* qmean, void* stream);
+
+/* Rescue token of every (query tile t, key block j < t, q head): the position p of
+ * the block maximising qmean[t, h] . k[j, p] (fp32 dot products; the first position
+ * on ties). qmean from spx_tile_mean_query; key_tiles from spx_block_pool.
+ * choice: uint8 [B, NB, NB, Hq] contiguous, 0 where j >= t.
+ * Replaces kernels.py:277-283 (token_scores / argmax inside rescue_tail). */
+int spx_rescue_choice(const float* qmean, const void* key_tiles, int batch, int seq, int q_heads,
+                      int kv_heads, int head_dim, int block_size, uint8_t* choice, void* stream);
+
+/* Rescue path alone: fp32 output and natural-log LSE of each row against one entry
+ * per unselected full-history block of its tile (the block's rescue token: its key
+ * and value, logit scale q.k) and, with remainder != 0, a second entry with the mean
+ * K / V of the block's other 127 tokens (logit + ln 127). Selection as index lists;
+ * mean_k / mean_v (fp32 [B, NB, Hkv, D], from spx_block_descriptors) are read only
+ * with remainder. Replaces kernels.py:233-309 (rescue_tail). */
+int spx_rescue_tail(const void* q, const int64_t* q_strides, const void* key_tiles,
+                    const void* value_tiles, const int64_t* indices, const int64_t* index_strides,
+                    const int32_t* counts, const int64_t* count_strides, const uint8_t* choice,
+                    const float* mean_k, const float* mean_v, int remainder, int batch, int seq,
+                    int q_heads, int kv_heads, int head_dim, int block_size, float scale,
+                    float* out, const int64_t* out_strides, float* lse,
+                    const int64_t* lse_strides, void* stream);
+
+/* Exact attention with the rescue path fused into the same online softmax (equal
+ * to the logaddexp merge of the two). Replaces the exact + rescue + merge stages of
+ * attention.py:306-331 (fp_v1_rescue / fp_v1_rescue_v2): upstream exact_attention,
+ * kernels.py:233-309 (rescue_tail) and kernels.py:312-325 (merge_exact_mean). */
+int spx_sparse_attention_rescue(const void* q, const int64_t* q_strides, const void* key_tiles,
+                                const void* value_tiles, const int64_t* indices,
+                                const int64_t* index_strides, const int32_t* counts,
+                                const int64_t* count_strides, const uint8_t* choice,
+                                const float* mean_k, const float* mean_v, int remainder,
+                                int batch, int seq, int q_heads, int kv_heads, int head_dim,
+                                int block_size, float scale, void* out,
+                                const int64_t* out_strides, float* lse,
+                                const int64_t* lse_strides, void* stream);
 
 /* ----------------------------------------------------------- accounting */
 

@@ -39,9 +39,12 @@ METHODS = (
     "mean_balanced",
     "cgf_mean",
     "dispersion_mean",
+    "fp_v1_rescue",
+    "fp_v1_rescue_v2",
 )
-V1_ROUTED = {"fp_v1", "mean_native"}
+V1_ROUTED = {"fp_v1", "mean_native", "fp_v1_rescue", "fp_v1_rescue_v2"}
 MEAN_METHODS = {"mean_native", "mean_balanced", "cgf_mean", "dispersion_mean"}
+RESCUE_METHODS = {"fp_v1_rescue", "fp_v1_rescue_v2"}
 SELECTORS = ("mean_balanced", "cgf_mean", "dispersion_mean")
 
 _F32 = np.float32
@@ -481,6 +484,102 @@ def merge_exact_mean(exact_output, exact_lse, mean_output, mean_lse):
     return bf16_round(output.astype(np.float32)), total.astype(np.float32)
 
 
+# ------------------------------------------------------------ rescue tail
+
+def tile_mean_query(q, block_size: int = BLOCK_SIZE, precision: str = "f64"):
+    """Mean query of every query tile over its real rows, float32
+    ``[B, NB, Hq, D]`` (kernels.py:274-276: sum over the tile / real row count)."""
+    acc = _acc(precision)
+    batch, sequence, q_heads, dim = q.shape
+    blocks = num_blocks(sequence, block_size)
+    out = np.zeros((batch, blocks, q_heads, dim), dtype=np.float32)
+    for t in range(blocks):
+        rows = q[:, t * block_size:min(sequence, (t + 1) * block_size)].astype(acc)
+        out[:, t] = (rows.sum(axis=1) / acc(rows.shape[1])).astype(np.float32)
+    return out
+
+
+def rescue_choice(q, k, block_size: int = BLOCK_SIZE, precision: str = "f64"):
+    """Rescue token of every (query tile t, key block j < t, q head):
+    argmax over the block's 128 positions of qbar_t . k (kernels.py:277-283), the
+    first position on ties (torch.argmax). uint8 ``[B, NB, NB, Hq]`` (0 for j >= t).
+    Positions past the sequence end hold zero keys, as the reference's padding."""
+    acc = _acc(precision)
+    batch, sequence, q_heads, dim = q.shape
+    kv_heads = k.shape[2]
+    group = q_heads // kv_heads
+    blocks = num_blocks(sequence, block_size)
+    qbar = tile_mean_query(q, block_size, precision).astype(acc)
+    kb = _pad_blocks(k, block_size).astype(acc)          # [B, NB, blk, Hkv, D]
+    choice = np.zeros((batch, blocks, blocks, q_heads), dtype=np.uint8)
+    for b in range(batch):
+        for h in range(q_heads):
+            g = h // group
+            # scores[t, j, pos] = qbar[t] . k[j, pos]
+            scores = np.einsum("td,jpd->tjp", qbar[b, :, h], kb[b, :, :, g])
+            if precision == "f32":
+                scores = scores.astype(np.float32)
+            best = scores.argmax(axis=2)                    # first maximum on ties
+            causal = np.arange(blocks)[None, :] < np.arange(blocks)[:, None]
+            choice[b, :, :, h] = np.where(causal, best, 0).astype(np.uint8)
+    return choice
+
+
+def rescue_tail(q, k, v, selected, scale, block_size: int = BLOCK_SIZE, remainder: bool = False,
+                precision: str = "f64", tiles=None, choice=None):
+    """Exact attention to one rescue token per unselected full-history block
+    (kernels.py:233-309), in float32 outputs.
+
+    Row r of tile t, head h, tail = {j < t : not selected[t, j, h]}: entry j is the
+    block's rescue token (``rescue_choice``) with logit scale * q.k_tok and value
+    v_tok; with ``remainder`` block j adds a second entry, the mean K / V of its
+    other B - 1 tokens, with logit scale * q.k_rest + ln(B - 1). Returns the
+    softmax-weighted output and the natural-log LSE over these entries (0 / -inf
+    for an empty tail). ``choice`` may be given (the GPU's), to test the attention
+    part on identical tokens.
+    """
+    acc = _acc(precision)
+    batch, sequence, q_heads, dim = q.shape
+    kv_heads = k.shape[2]
+    group = q_heads // kv_heads
+    blocks = num_blocks(sequence, block_size)
+    if choice is None:
+        choice = rescue_choice(q, k, block_size, precision)
+    kb = _pad_blocks(k, block_size).astype(acc)
+    vb = _pad_blocks(v, block_size).astype(acc)
+    rows = np.arange(sequence)
+    if tiles is not None:
+        rows = np.concatenate([np.arange(t * block_size, min(sequence, (t + 1) * block_size))
+                               for t in tiles])
+    out = np.zeros((batch, sequence, q_heads, dim), dtype=np.float32)
+    lse = np.full((batch, sequence, q_heads), -np.inf, dtype=np.float32)
+    log_rest = acc(math.log(block_size - 1))
+    for b in range(batch):
+        for h in range(q_heads):
+            g = h // group
+            for t in sorted(set((rows // block_size).tolist())):
+                tail = [j for j in range(t) if not selected[b, t, j, h]]
+                r = rows[(rows // block_size) == t]
+                if not tail:
+                    continue
+                tok = choice[b, t, tail, h].astype(np.int64)
+                keys = kb[b, tail, tok, g]                     # [n, D]
+                values = vb[b, tail, tok, g]
+                logits = (q[b, r, h].astype(acc) @ keys.T) * acc(scale)
+                if remainder:
+                    k_rest = (kb[b, tail, :, g].sum(axis=1) - keys) / acc(block_size - 1)
+                    v_rest = (vb[b, tail, :, g].sum(axis=1) - values) / acc(block_size - 1)
+                    rest = (q[b, r, h].astype(acc) @ k_rest.T) * acc(scale) + log_rest
+                    logits = np.concatenate([logits, rest], axis=1)
+                    values = np.concatenate([values, v_rest], axis=0)
+                row_max = logits.max(axis=1, keepdims=True)
+                weights = np.exp(logits - row_max)
+                total = weights.sum(axis=1, keepdims=True)
+                lse[b, r, h] = (row_max + np.log(total))[:, 0].astype(np.float32)
+                out[b, r, h] = ((weights / total) @ values).astype(np.float32)
+    return out, lse
+
+
 # --------------------------------------------------------------- accounting
 
 def selection_accounting(selected, sequence, q_tile_size, k_tile_size, method,
@@ -583,6 +682,11 @@ def attention_layer(q, k, v, scale, method, alpha=0.08, sink=2, window=4, last=2
     if method in MEAN_METHODS:
         mean_out, mean_lse = mean_tail(q, descriptors, selected, scale, block_size, precision)
         out, lse = merge_exact_mean(out, lse, mean_out, mean_lse)
+    elif method in RESCUE_METHODS:
+        r_out, r_lse = rescue_tail(q, k, v, selected, scale, block_size,
+                                   remainder=method == "fp_v1_rescue_v2", precision=precision,
+                                   tiles=tiles)
+        out, lse = merge_exact_mean(out, lse, r_out, r_lse)
     result.update(output=out, lse=lse, scores=scores, indices=indices, counts=counts,
                   selected=selected)
     return result

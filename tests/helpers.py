@@ -28,16 +28,19 @@ def to_np(t: torch.Tensor) -> np.ndarray:
     return t.float().cpu().numpy()
 
 
-def assert_output_close(actual, expected, max_abs=OUT_MAX_ABS, mean_abs=OUT_MEAN_ABS, what="output"):
+def assert_output_close(actual, expected, max_abs=OUT_MAX_ABS, mean_abs=OUT_MEAN_ABS, what="output",
+                        rel=0.0):
+    """max |a - e| - rel |e| <= max_abs and mean |a - e| <= mean_abs; ``rel`` = 2^-7
+    admits one bf16 output rounding step for outputs beyond unit scale."""
     a = np.asarray(actual, dtype=np.float64)
     e = np.asarray(expected, dtype=np.float64)
     assert a.shape == e.shape, (a.shape, e.shape)
     assert np.isfinite(a).all(), f"{what}: non-finite values"
     diff = np.abs(a - e)
-    worst = float(diff.max()) if diff.size else 0.0
+    worst = float((diff - rel * np.abs(e)).max()) if diff.size else 0.0
     mean = float(diff.mean()) if diff.size else 0.0
     assert worst <= max_abs and mean <= mean_abs, \
-        f"{what}: max-abs {worst:.3g} (limit {max_abs}), mean-abs {mean:.3g} (limit {mean_abs})"
+        f"{what}: max-abs {worst:.3g} (limit {max_abs}, rel {rel}), mean-abs {mean:.3g} (limit {mean_abs})"
     return worst, mean
 
 

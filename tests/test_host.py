@@ -26,7 +26,7 @@ def declared_symbols():
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     declared = declared_symbols()
-    assert len(declared) >= 17
+    assert len(declared) >= 21
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
     assert set(declared) == set(_lib.EXPORTED_SYMBOLS)
@@ -81,8 +81,11 @@ def test_reference_interface():
     assert up.attention_tile_sizes() == (128, 128) and up.score_tile_size() == 32
     with pytest.raises(ValueError, match="unsupported selector"):
         kernels.selector_scores(torch.zeros(1, 8, 1, 128), None, 0.1, "bogus")
-    with pytest.raises(NotImplementedError):
-        kernels.rescue_tail()
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        kernels.rescue_tail(torch.zeros(1, 8, 1, 128, dtype=torch.bfloat16),
+                            torch.zeros(1, 8, 1, 128, dtype=torch.bfloat16),
+                            torch.zeros(1, 8, 1, 128, dtype=torch.bfloat16),
+                            torch.zeros(1, 1, 1, 1, dtype=torch.bool), 0.1)
 
 
 def test_backend_registers_as_sdpa():
@@ -107,7 +110,7 @@ def test_wrappers_refuse_cpu_tensors():
     with pytest.raises(ValueError, match="ROCm GPU"):
         b.forward(L(), q, k.transpose(1, 2), k.transpose(1, 2), None, 0.1)
     b.configure("fp_v1_rescue")
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="ROCm GPU"):
         b.forward(L(), q, k.transpose(1, 2), k.transpose(1, 2), None, 0.1)
 
 

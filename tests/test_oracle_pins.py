@@ -465,5 +465,109 @@ def test_attention_layer_method_relations():
     dense = ref.attention_layer(q, k, v, 0.25, "dense")
     d_out, _ = dense_reference(q, k, v, 0.25)
     np.testing.assert_array_equal(dense["output"], ref.bf16_round(d_out.astype(np.float32)))
+    for rescue in ("fp_v1_rescue", "fp_v1_rescue_v2"):                   # same V1 routing
+        np.testing.assert_array_equal(ref.attention_layer(q, k, v, 0.25, rescue, 0.5)["selected"],
+                                      fp["selected"])
     with pytest.raises(ValueError):
-        ref.attention_layer(q, k, v, 0.25, "fp_v1_rescue")
+        ref.attention_layer(q, k, v, 0.25, "topk")
+
+
+# ----------------------------------------------------------- rescue tail
+
+def explicit_rescue_reference(q, k, v, selected, scale, remainder, block=128):
+    """check_math.py:122-162: token-mask exact attention plus, per unselected
+    full-history block, its argmax_j qbar.k_j token (and with ``remainder`` the
+    mean K / V of the other B-1 tokens with multiplicity B-1), float64 loops."""
+    _, sequence, heads, dim = q.shape
+    group = heads // k.shape[2]
+    keys = np.repeat(k[0], group, 1).astype(np.float64)
+    values = np.repeat(v[0], group, 1).astype(np.float64)
+    queries = q[0].astype(np.float64)
+    pos = np.arange(sequence)
+    out = np.zeros((sequence, heads, dim))
+    lse = np.zeros((sequence, heads))
+    for tile in range(selected.shape[1]):
+        rows = np.arange(tile * block, min(sequence, (tile + 1) * block))
+        for head in range(heads):
+            allowed = selected[0, tile, pos // block, head][None, :] & (pos[None, :] <= rows[:, None])
+            logits = [np.where(allowed, queries[rows, head] @ keys[:, head].T * scale, -np.inf)]
+            parts = [values[:, head]]
+            qbar = queries[rows, head].mean(axis=0)
+            for key_block in range(tile):
+                if selected[0, tile, key_block, head]:
+                    continue
+                span = slice(key_block * block, (key_block + 1) * block)
+                bk, bv = keys[span, head], values[span, head]
+                choice = int(np.argmax(bk @ qbar))
+                logits.append(queries[rows, head] @ bk[choice][:, None] * scale)
+                parts.append(bv[choice][None])
+                if remainder:
+                    rest = np.arange(block) != choice
+                    logits.append(queries[rows, head] @ bk[rest].mean(axis=0)[:, None] * scale
+                                  + np.log(block - 1.0))
+                    parts.append(bv[rest].mean(axis=0)[None])
+            z = np.concatenate(logits, axis=1)
+            m = z.max(axis=1, keepdims=True)
+            w = np.exp(z - m)
+            lse[rows, head] = (m + np.log(w.sum(axis=1, keepdims=True)))[:, 0]
+            out[rows, head] = (w / w.sum(axis=1, keepdims=True)) @ np.concatenate(parts, axis=0)
+    return out[None], lse[None]
+
+
+def _rescue_fixture():
+    """check_math.py:252-262: 385 tokens (4 tiles, the last has one row), fixed mask."""
+    q, k, v = rnd((1, 385, 4, 8), 40), rnd((1, 385, 2, 8), 41), rnd((1, 385, 2, 8), 42)
+    sel = ref.protected_selection(np.zeros((1, 4, 4, 4), np.float32), 0.0, 2, 4, 2)
+    sel[:, 2, 0, ::2] = False
+    sel[:, 2, 1, 1::2] = False
+    sel[:, 3, 1, :] = False
+    return q, k, v, sel
+
+
+@pytest.mark.parametrize("remainder", (False, True))
+def test_exact_plus_rescue_against_check_math(remainder):
+    q, k, v, sel = _rescue_fixture()
+    idx, cnt = ref.indices_from_mask(sel)
+    merged, total = ref.merge_exact_mean(*ref.exact_attention(q, k, v, idx, cnt, SCALE),
+                                         *ref.rescue_tail(q, k, v, sel, SCALE, remainder=remainder))
+    want, want_total = explicit_rescue_reference(q, k, v, sel, SCALE, remainder)
+    np.testing.assert_allclose(merged, want, atol=0.03, rtol=0.03)       # check_math.py:281-282
+    np.testing.assert_allclose(total, want_total, atol=1e-5)
+    # rows of tiles 0-1 have no unselected history: the rescue LSE is -inf there
+    _, r_lse = ref.rescue_tail(q, k, v, sel, SCALE, remainder=remainder)
+    assert (r_lse[:, :256] == -np.inf).all() and np.isfinite(r_lse[:, 256:]).all()
+
+
+def test_rescue_choice_loop_ties_and_future_invariance():
+    q, k = rnd((1, 300, 4, 8), 43), rnd((1, 300, 2, 8), 44)
+    choice = ref.rescue_choice(q, k)
+    for t, j, h in itertools.product(range(3), range(3), range(4)):
+        if j >= t:
+            assert choice[0, t, j, h] == 0
+            continue
+        rows = q[0, t * 128:min(300, t * 128 + 128), h].astype(np.float64)
+        qbar = rows.sum(axis=0) / len(rows)
+        scores = k[0, j * 128:(j + 1) * 128, h // 2].astype(np.float64) @ qbar
+        assert choice[0, t, j, h] == int(np.argmax(scores))
+    # exact ties pick the first position: two identical maximal keys in block 0
+    k2 = np.zeros((1, 300, 2, 8), np.float32)
+    k2[0, 5, 0] = k2[0, 77, 0] = 1.0
+    q2 = np.ones((1, 300, 4, 8), np.float32)
+    assert ref.rescue_choice(q2, k2)[0, 1, 0, 0] == 5
+    # all scores equal (zero keys): position 0
+    assert ref.rescue_choice(q2, np.zeros_like(k2))[0, 2, 1, 3] == 0
+
+
+@pytest.mark.parametrize("remainder", (False, True))
+def test_rescue_future_kv_invariance_and_all_selected(remainder):
+    q, k, v, sel = _rescue_fixture()
+    out, lse = ref.rescue_tail(q, k, v, sel, SCALE, remainder=remainder)
+    k2, v2 = k.copy(), v.copy()
+    k2[:, 300:] *= 19                                                    # check_math.py:283-287
+    v2[:, 300:] += 23
+    out2, lse2 = ref.rescue_tail(q, k2, v2, sel, SCALE, remainder=remainder)
+    np.testing.assert_array_equal(out2[:, :300], out[:, :300])
+    np.testing.assert_array_equal(lse2[:, :300], lse[:, :300])
+    full = ref.protected_selection(np.zeros((1, 4, 4, 4), np.float32), 0.0, 2, 4, 2)
+    f_out, f_lse = ref.rescue_tail(q, k, v, full, SCALE, remainder=remainder)
+    assert (f_lse == -np.inf).all() and (f_out == 0).all()
