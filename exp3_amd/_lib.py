@@ -18,7 +18,7 @@ SPX_OK = 0
 SPX_EINVAL = -1
 SPX_EUNSUPPORTED = -2
 SPX_ELAUNCH = -3
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 SELECTOR_IDS = {"mean_balanced": 0, "cgf_mean": 1, "dispersion_mean": 2}
 
@@ -39,7 +39,8 @@ _PROTOTYPES = {
                      _P, _P],
     "spx_indices_from_mask": [_P, _I, _I, _I, _I, _P, _P, _P],
     "spx_mask_from_indices": [_P, _P, _I, _I, _I, _I, _P, _P],
-    "spx_selector_scores": [_P, _S, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _S, _P],
+    "spx_selector_scores": [_P, _S, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P, _P, _S,
+                            _P],
     "spx_exact_attention": [_P, _S, _P, _P, _P, _S, _P, _S, _I, _I, _I, _I, _I, _I, _F, _P,
                             _S, _P, _S, _P],
     "spx_sparse_attention_mean": [_P, _S, _P, _P, _P, _S, _P, _S, _P, _P, _P, _I, _I, _I, _I,
@@ -56,7 +57,11 @@ _PROTOTYPES = {
                                     _I, _I, _I, _F, _P, _S, _P, _S, _P],
 }
 
-EXPORTED_SYMBOLS = tuple(_PROTOTYPES) + ("spx_last_error", "spx_abi_version")
+# helpers with other return types
+_SIZE_FUNCTIONS = {"spx_selector_workspace_bytes": [_I, _I, _I, _I]}
+
+EXPORTED_SYMBOLS = tuple(_PROTOTYPES) + tuple(_SIZE_FUNCTIONS) + ("spx_last_error",
+                                                                   "spx_abi_version")
 
 _lib = None
 
@@ -79,6 +84,10 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = argtypes
         fn.restype = ctypes.c_int
+    for name, argtypes in _SIZE_FUNCTIONS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int64
     if lib.spx_abi_version() != ABI_VERSION:
         raise RuntimeError(f"exp3_amd ABI mismatch: library {lib.spx_abi_version()}, "
                            f"bindings {ABI_VERSION}; rebuild the library")

@@ -588,7 +588,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
 
   // ---- membership bitmaps of both items' lists (valid ids), then their union
   if (tid < 2 * (kMaxBlocksAttn / 32)) (&bits[0][0])[tid] = 0u;
-  __syncthreads();
+  block_sync();
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int tt = t_item[it];
@@ -605,7 +605,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
       for (int j = tid; j <= tt; j += kAttnThreads) atomicOr(&bits[it][j >> 5], 1u << (j & 31));
     }
   }
-  __syncthreads();
+  block_sync();
   // Processing order: every listed block except the two diagonal ones (t, t - 1),
   // ascending, then the diagonal ones. The block loop for the first part has a
   // single (unmasked) code path, which keeps O in one register set.
@@ -620,7 +620,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
       const uint64_t ballot = __ballot(flag);
       const int before = __popcll(ballot & ((1ull << lane) - 1ull));
       if (lane == 0) wave_counts[w] = __popcll(ballot);
-      __syncthreads();
+      block_sync();
       int offset = nu;
       for (int x = 0; x < w; ++x) offset += wave_counts[x];
       if (flag) {
@@ -628,7 +628,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
         uflag[offset + before] = (uint8_t)f;
       }
       for (int x = 0; x < kAttnThreads / 64; ++x) nu += wave_counts[x];
-      __syncthreads();
+      block_sync();
     }
   };
   compact(false);
@@ -649,7 +649,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
     // block u + 1 into the other buffers, where it lands during block u's math.
     auto begin_block = [&](int u) {
       wait_tiles();
-      __syncthreads();  // block u visible to all; every wave is done with block u - 1
+      block_sync();  // block u visible to all; every wave is done with block u - 1
       if (u + 1 < nu) {
         const int jn = __builtin_amdgcn_readfirstlane(ulist[u + 1]);
         dma_tile(kbase + jn * tile_elems, kbuf[(u + 1) & 1], tid);
@@ -664,7 +664,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
       constexpr int B = decltype(buf)::value;
       const int f = __builtin_amdgcn_readfirstlane(uflag[uu]);
       wait_tiles();
-      __syncthreads();  // block uu visible to all; every wave is done with block uu - 1
+      block_sync();  // block uu visible to all; every wave is done with block uu - 1
       NextCopy nx;
       nx.any = uu + 1 < nu;
       const int jn = nx.any ? __builtin_amdgcn_readfirstlane(ulist[uu + 1]) : 0;
@@ -701,7 +701,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
         }
       }
     }
-    __syncthreads();  // every wave is done with the last block
+    block_sync();  // every wave is done with the last block
   }
 
   if (TAIL) {
@@ -718,26 +718,26 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
         const uint64_t ballot = __ballot(in_tail);
         const int before = __popcll(ballot & ((1ull << lane) - 1ull));
         if (lane == 0) wave_counts[w] = __popcll(ballot);
-        __syncthreads();
+        block_sync();
         int offset = ntail[it];
         for (int x = 0; x < w; ++x) offset += wave_counts[x];
         if (in_tail) tlist[it][offset + before] = (int16_t)j;
         for (int x = 0; x < kAttnThreads / 64; ++x) ntail[it] += wave_counts[x];
-        __syncthreads();
+        block_sync();
       }
     }
     const int64_t desc_base = (int64_t)b * a.blocks * a.kv_heads + g;  // (b, 0, g)
     const int nmax = max(ntail[0], ntail[1]);
     const int epb = a.tail_kind == 2 ? 2 : 1;   // tail entries per unselected block
     for (int t0 = 0; t0 < nmax; t0 += kTailTile / epb) {
-      __syncthreads();
+      block_sync();
       if (a.tail_kind == 0)
         stage_tail(a, tlist[item], ntail[item], t0, desc_base, kbuf[item], vbuf[item],
                    tail_bias[item], tid & (kItemWaves * 64 - 1), kItemWaves * 64);
       else
         stage_rescue(a, tlist[item], ntail[item], t0, epb, b, g, h, t, kbuf[item], vbuf[item],
                      tail_bias[item], tid & (kItemWaves * 64 - 1), kItemWaves * 64);
-      __syncthreads();
+      block_sync();
       if (t0 < ntail[item]) {
         f32x16 s[4];
         bf16x8 pb[8];

@@ -52,14 +52,14 @@ __global__ __launch_bounds__(256) void accounting_kernel(const uint8_t* mask, in
   red[0][threadIdx.x] = pairs;
   red[1][threadIdx.x] = selected;
   red[2][threadIdx.x] = tail;
-  __syncthreads();
+  block_sync();
   for (int s = 128; s > 0; s >>= 1) {
     if ((int)threadIdx.x < s) {
       red[0][threadIdx.x] += red[0][threadIdx.x + s];
       red[1][threadIdx.x] += red[1][threadIdx.x + s];
       red[2][threadIdx.x] += red[2][threadIdx.x + s];
     }
-    __syncthreads();
+    block_sync();
   }
   if (threadIdx.x == 0) {
     atomicAdd(reinterpret_cast<unsigned long long*>(&totals[0]), (unsigned long long)red[0][0]);

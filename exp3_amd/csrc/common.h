@@ -85,6 +85,16 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Workgroup barrier preceded by an explicit wait for this wave's outstanding LDS
+// operations. __syncthreads() alone is not enough: at a loop-header barrier whose
+// back edge carries an LDS store, hipcc has emitted s_barrier with the store still
+// in flight, and another wave then read the old value right after the barrier.
+// Every kernel here synchronises through this helper.
+__device__ __forceinline__ void block_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __syncthreads();
+}
+
 // --------------------------------------------------------------- geometry
 
 __host__ __device__ __forceinline__ int num_blocks(int seq) { return (seq + kBlock - 1) / kBlock; }

@@ -113,7 +113,7 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
       if (DO_V) { part[2][wave][d] = sv[e]; part[3][wave][d] = qv[e]; }
     }
   }
-  __syncthreads();
+  block_sync();
 
   if (tid < kHeadDim) {
     const int d = tid;
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
     }
   }
   if (DO_V) {
-    __syncthreads();
+    block_sync();
     if (a.sigma_v && tid == 0)
       a.sigma_v[((int64_t)b * a.blocks + j) * a.kv_heads + g] = sqrtf(sig_part[0] + sig_part[1]);
   }

@@ -96,7 +96,7 @@ __global__ __launch_bounds__(kBlock) void rescue_choice_kernel(ChoiceArgs a) {
   for (int t = j + 1; t < a.blocks; ++t) {
     const float* qm = a.qmean + (((int64_t)b * a.blocks + t) * a.q_heads + g * a.group) * kHeadDim;
     for (int i = tok; i < a.group * kHeadDim; i += kBlock) qs[i] = qm[i];
-    __syncthreads();
+    block_sync();
     for (int hh = 0; hh < a.group; ++hh) {
       float s = 0.0f;
 #pragma unroll
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kBlock) void rescue_choice_kernel(ChoiceArgs a) {
       }
       if (lane == 0) best[w][hh] = key;
     }
-    __syncthreads();
+    block_sync();
     if (tok < a.group) {
       const uint64_t k0 = best[0][tok], k1 = best[1][tok];
       const uint64_t k = k0 > k1 ? k0 : k1;

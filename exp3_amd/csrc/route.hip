@@ -45,9 +45,9 @@ struct SelectOut {
 __device__ __forceinline__ float block_reduce_max(float v, float* scratch) {
   v = wave_max(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
+  block_sync();
   if (lane == 0) scratch[wave] = v;
-  __syncthreads();
+  block_sync();
   float r = scratch[0];
   for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = max_nan(r, scratch[w]);
   return r;
@@ -56,9 +56,9 @@ __device__ __forceinline__ float block_reduce_max(float v, float* scratch) {
 __device__ __forceinline__ float block_reduce_sum(float v, float* scratch) {
   v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __syncthreads();
+  block_sync();
   if (lane == 0) scratch[wave] = v;
-  __syncthreads();
+  block_sync();
   float r = scratch[0];
   for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r += scratch[w];
   return r;
@@ -115,9 +115,9 @@ __device__ void select_row(const float* row, int t, const SelectParams& p, const
     }
     const uint64_t ballot = __ballot(active);
     const int before = __popcll(ballot & ((1ull << lane) - 1ull));
-    __syncthreads();
+    block_sync();
     if (lane == 0) wave_counts[wave] = __popcll(ballot);
-    __syncthreads();
+    block_sync();
     int offset = base;
     for (int w = 0; w < wave; ++w) offset += wave_counts[w];
     if (active && o.indices) o.indices[o.row_base + (int64_t)(offset + before) * o.heads] = j;
@@ -229,7 +229,7 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
       part_max[wave][col] = mx;
       part_mass[wave][col] = mass;
     }
-    __syncthreads();
+    block_sync();
     if (tid < 32) {
       float m = part_max[0][tid];
       for (int w = 1; w < 4; ++w) m = fmaxf(m, part_max[w][tid]);
@@ -246,7 +246,7 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
         blk_mass[jj] = s;
       }
     }
-    __syncthreads();
+    block_sync();
   }
 
   // normalize_scores over j <= t; j > t has M = -inf and contributes 0.
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
     if (a.score) a.score[b * a.ss_b + t * a.ss_t + jj * a.ss_j + h * a.ss_h] = s;
   }
   if (a.indices) {
-    __syncthreads();
+    block_sync();
     SelectOut o;
     o.indices = a.indices;
     o.counts = a.counts;
@@ -301,7 +301,7 @@ __global__ __launch_bounds__(kRouteThreads) void select_kernel(SelectArgs a) {
   const int kb = a.sel.key_blocks;
   for (int j = threadIdx.x; j < kb; j += blockDim.x)
     row[j] = a.score[b * a.ss_b + t * a.ss_t + j * a.ss_j + h * a.ss_h];
-  __syncthreads();
+  block_sync();
   SelectOut o;
   o.indices = a.indices;
   o.counts = a.counts;
@@ -336,9 +336,9 @@ __global__ __launch_bounds__(kRouteThreads) void indices_from_mask_kernel(MaskAr
     const bool active = j < kb && a.mask[row_base + (int64_t)j * a.heads] != 0;
     const uint64_t ballot = __ballot(active);
     const int before = __popcll(ballot & ((1ull << lane) - 1ull));
-    __syncthreads();
+    block_sync();
     if (lane == 0) wave_counts[wave] = __popcll(ballot);
-    __syncthreads();
+    block_sync();
     int offset = base;
     for (int w = 0; w < wave; ++w) offset += wave_counts[w];
     if (active) a.indices[row_base + (int64_t)(offset + before) * a.heads] = j;
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(kRouteThreads) void mask_from_indices_kernel(MaskAr
   const int64_t row_base = (((int64_t)b * a.query_blocks + t) * kb) * a.heads + h;
   uint8_t* mask = a.mask;
   for (int j = threadIdx.x; j < kb; j += blockDim.x) mask[row_base + (int64_t)j * a.heads] = 0;
-  __syncthreads();
+  block_sync();
   const int count = min(max(cnt[((int64_t)b * a.query_blocks + t) * a.heads + h], 0), kb);
   for (int p = threadIdx.x; p < count; p += blockDim.x) {
     const int64_t j = idx[row_base + (int64_t)p * a.heads];

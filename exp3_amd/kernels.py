@@ -95,10 +95,14 @@ def selector_scores(q: torch.Tensor, descriptors: BlockDescriptors, scale: float
     sigma_v = descriptors.sigma_v.contiguous()
     counts = descriptors.counts.to(torch.int32).contiguous()
     scores = torch.empty(batch, blocks, blocks, q_heads, dtype=torch.float32, device=device)
+    nbytes = _lib.load().spx_selector_workspace_bytes(batch, sequence, kv_heads, head_dim)
+    if nbytes < 0:
+        raise ValueError(f"selector_scores: unsupported shape {tuple(q.shape)}")
+    workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
     _lib.call("spx_selector_scores", _lib.ptr(q), _lib.strides(q), _lib.ptr(mean_k),
               _lib.ptr(var_k), _lib.ptr(sigma_v), _lib.ptr(counts), batch, sequence, q_heads,
               kv_heads, head_dim, block_size, _lib.SELECTOR_IDS[selector], float(scale),
-              _lib.ptr(scores), _lib.strides(scores), _lib.stream(device))
+              _lib.ptr(workspace), _lib.ptr(scores), _lib.strides(scores), _lib.stream(device))
     return scores
 
 

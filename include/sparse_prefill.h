@@ -37,7 +37,7 @@ extern "C" {
 #define SPX_EUNSUPPORTED (-2) /* valid in the reference, not built here       */
 #define SPX_ELAUNCH (-3)      /* HIP launch / runtime failure                 */
 
-#define SPX_ABI_VERSION 3
+#define SPX_ABI_VERSION 4
 
 /* Selector ids for spx_selector_scores (kernels.py:62). */
 #define SPX_SELECTOR_MEAN_BALANCED 0
@@ -139,12 +139,19 @@ int spx_mask_from_indices(const int64_t* indices, const int32_t* counts, int bat
 /* Balanced / CGF / dispersion block scores (selector = SPX_SELECTOR_*), written to
  * score (strided [B, NB, NB, Hq] fp32, every entry written).
  * mean_k, var_k: contiguous fp32 [B, NB, Hkv, D]; sigma_v [B, NB, Hkv];
- * counts [NB] int32. Replaces kernels.py:49-126 (selector_scores). */
+ * counts [NB] int32. workspace: caller-allocated device memory of
+ * spx_selector_workspace_bytes() bytes, 16-byte aligned (the bf16 hi/lo split of
+ * mean_k and var_k, rewritten by every call; calls that overlap on one workspace
+ * race). Replaces kernels.py:49-126 (selector_scores). */
 int spx_selector_scores(const void* q, const int64_t* q_strides, const float* mean_k,
                         const float* var_k, const float* sigma_v, const int32_t* counts,
                         int batch, int seq, int q_heads, int kv_heads, int head_dim,
-                        int block_size, int selector, float scale, float* score,
-                        const int64_t* score_strides, void* stream);
+                        int block_size, int selector, float scale, void* workspace,
+                        float* score, const int64_t* score_strides, void* stream);
+
+/* Bytes of the spx_selector_scores workspace (B * Hkv * ceil(NB / 32) * 32 KB), or -1
+ * for an unsupported shape. Helper of spx_selector_scores (no reference counterpart). */
+int64_t spx_selector_workspace_bytes(int batch, int seq, int kv_heads, int head_dim);
 
 /* ----------------------------------------------------------- attention */
 

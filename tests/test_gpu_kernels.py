@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from exp3_amd import kernels
+from exp3_amd import kernels, synthetic
 from exp3_amd.upstream import flashprefill_native_forward as up
 from oracle import reference_cpu as ref
 from tests.helpers import (SCALE, assert_output_close, inputs, masks_equal_except_ties,
@@ -147,7 +147,7 @@ def test_protected_selection_bit_exact(gpu, length):
         np.testing.assert_array_equal(to_np(back), expected)
 
 
-@pytest.mark.parametrize("length", (257, 1089))
+@pytest.mark.parametrize("length", (257, 1089, 4500))   # 4500: 36 blocks, two 32-block chunks
 @pytest.mark.parametrize("selector", ("mean_balanced", "cgf_mean", "dispersion_mean"))
 def test_selector_scores(gpu, length, selector):
     q, k, v = inputs(length, seed=41)
@@ -158,6 +158,31 @@ def test_selector_scores(gpu, length, selector):
                                     ("mean_k", "mean_v", "var_k", "sigma_v", "counts")))
     expected = ref.selector_scores(to_np(q), e_desc, SCALE, selector)
     np.testing.assert_allclose(actual, expected, atol=2e-5, rtol=2e-5)   # check_math.py:287-290
+
+
+@pytest.mark.parametrize("selector", ("mean_balanced", "cgf_mean", "dispersion_mean"))
+def test_selector_scores_full_size_repeatable(gpu, selector):
+    """S=32640 (255 tiles, 8 chunks of 32 blocks): every call gives the same bits,
+    also after short sequences that leave other values in LDS, and for the two
+    softmax-mean selectors every tile's scores over j < t sum to 1 (mean of softmax
+    rows). A cross-wave LDS race once left one tile's first chunk with another
+    workgroup's partial sums (row sum 1.22)."""
+    q, k, v, _ = synthetic.make_inputs(32640, seed=23, device="cuda")
+    desc = kernels.block_descriptors(k, v)
+    qs, ks, vs, _ = synthetic.make_inputs(1089, seed=5, device="cuda")
+    small = kernels.block_descriptors(ks, vs)
+    runs = []
+    for _ in range(4):
+        kernels.selector_scores(qs, small, SCALE, selector)
+        runs.append(kernels.selector_scores(q, desc, SCALE, selector))
+    first = runs[0].cpu()
+    for r in runs[1:]:
+        assert torch.equal(r.cpu(), first)
+    s = first[0].double().numpy()                    # [t, j, h]
+    blocks = s.shape[0]
+    assert np.all(s[np.triu_indices(blocks)[0], np.triu_indices(blocks)[1]] == 0)   # j >= t
+    if selector != "dispersion_mean":
+        np.testing.assert_allclose(s[1:].sum(axis=1), 1.0, atol=1e-5)
 
 
 def _fixed_selection(length, seed, drop=0.3):
