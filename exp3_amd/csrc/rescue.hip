@@ -9,18 +9,15 @@
 // gfx950 design
 //   * tile_mean_kernel: one thread per (q head, dim pair) and query tile, fp32 sums
 //     over the tile's rows (coalesced 4-byte reads along the head's dims).
-//   * rescue_choice_kernel: one workgroup per (key block j, kv group), one thread
-//     per token holding its key row in fp32 registers (read once from the key
-//     tile, which is already in the K layout); for every later tile t the group's
-//     mean queries are staged in LDS once and read by all threads as broadcasts,
-//     each token's dot products being plain fp32 FMAs. The argmax is a
-//     64-bit max over (order-preserving score bits, 127 - position) across the
-//     block, which also picks the first position on ties.
+//   * rescue_choice_kernel: the token scores of block j against every later tile's
+//     mean queries form a GEMM (128 tokens x 128 dims x (tiles, heads)); it runs on
+//     bf16 MFMA with the key tile (bf16-exact) staged in LDS and the fp32 means
+//     split exactly into three bf16 parts, followed by an in-register argmax.
 #include "common.h"
 
 namespace spx {
 
-constexpr int kMaxGroup = 8;
+constexpr int kChoiceThreads = 256;  // four waves
 
 struct MeanQArgs {
   const uint16_t* q;
@@ -57,68 +54,103 @@ struct ChoiceArgs {
   int batch, q_heads, kv_heads, blocks, group;
 };
 
-// float -> uint32 whose unsigned order is the float order (non-NaN values)
-__device__ __forceinline__ uint32_t order_key(float x) {
-  const uint32_t u = __float_as_uint(x);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+__device__ __forceinline__ bf16x8 pack_bf16x8(const float (&x)[8]) {
+  u32x4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = pack_bf16x2(x[2 * e], x[2 * e + 1]);
+  return as_bf16x8(r);
 }
 
-__global__ __launch_bounds__(kBlock) void rescue_choice_kernel(ChoiceArgs a) {
+// One workgroup per (key block j, kv group g, batch b). The key tile of block j
+// (pool layout: row = token, 16-byte chunk c of row r at c ^ (r & 15)) is staged in
+// LDS once; its 128 token rows are the MFMA A operand (four 32-row tiles). The
+// columns are the (later tile t, q head) pairs of the group, 32 per wave step; their
+// fp32 mean queries are split exactly into three bf16 parts (hi + mid + lo), so
+// three bf16 products per k-step give the fp32 dot products to ~2^-24 relative.
+// Each lane then owns one column's 128 token scores (64 per lane half, in token
+// order): a strict in-lane max keeps the first position, and the two halves merge
+// with the lower position on equal scores (torch.argmax: first maximum).
+__global__ __launch_bounds__(kChoiceThreads) void rescue_choice_kernel(ChoiceArgs a) {
   const int j = blockIdx.x;
   const int g = blockIdx.y;
   const int b = blockIdx.z;
-  const int tok = threadIdx.x;
-  const int lane = tok & 63, w = tok >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int col = lane & 31, half = lane >> 5;
   // entries of tiles t <= j (no rescue token) are written as 0
-  for (int i = tok; i < (j + 1) * a.group; i += kBlock) {
+  for (int i = tid; i < (j + 1) * a.group; i += kChoiceThreads) {
     const int t = i / a.group, hh = i % a.group;
     a.choice[(((int64_t)b * a.blocks + t) * a.blocks + j) * a.q_heads + g * a.group + hh] = 0;
   }
   if (j >= a.blocks - 1) return;  // no later tile
 
-  float kf[kHeadDim];
+  __shared__ __align__(16) uint16_t kt[kBlock * kHeadDim];  // 32 KB
   {
-    const uint16_t* row =
-        a.kt + ((((int64_t)b * a.kv_heads + g) * a.blocks + j) * kBlock + tok) * kHeadDim;
-#pragma unroll
-    for (int c = 0; c < kHeadDim / 8; ++c) {
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(row + ((c ^ (tok & 15)) << 3));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kf[8 * c + 2 * e] = bf16_lo(raw[e]);
-        kf[8 * c + 2 * e + 1] = bf16_hi(raw[e]);
-      }
-    }
+    const u32x4* src = reinterpret_cast<const u32x4*>(
+        a.kt + (((int64_t)b * a.kv_heads + g) * a.blocks + j) * kBlock * kHeadDim);
+    u32x4* dst = reinterpret_cast<u32x4*>(kt);
+    for (int i = tid; i < kBlock * kHeadDim / 8; i += kChoiceThreads) dst[i] = src[i];
   }
+  block_sync();
 
-  __shared__ __align__(16) float qs[kMaxGroup * kHeadDim];
-  __shared__ uint64_t best[2][kMaxGroup];
-  for (int t = j + 1; t < a.blocks; ++t) {
-    const float* qm = a.qmean + (((int64_t)b * a.blocks + t) * a.q_heads + g * a.group) * kHeadDim;
-    for (int i = tok; i < a.group * kHeadDim; i += kBlock) qs[i] = qm[i];
-    block_sync();
-    for (int hh = 0; hh < a.group; ++hh) {
-      float s = 0.0f;
+  const int ncols = a.group * (a.blocks - 1 - j);
+  const int ngroups = (ncols + 31) / 32;
+  // LDS element offset of token row (32 rt + col), chunk 2 dc + half:
+  // ((2 dc + half) ^ (col & 15)) << 3 = base ^ (dc << 4), plus rt * 32 rows
+  const int e0 = col * kHeadDim + (((col >> 1) & 7) << 4) + ((half ^ (col & 1)) << 3);
+  for (int grp = w; grp < ngroups; grp += kChoiceThreads / 64) {
+    const int c = grp * 32 + col;
+    const bool cok = c < ncols;
+    const int t = j + 1 + (cok ? c / a.group : 0);
+    const int hh = cok ? c % a.group : 0;
+    const float* qm = a.qmean + (((int64_t)b * a.blocks + t) * a.q_heads + g * a.group + hh) * kHeadDim +
+                      half * 8;
+    f32x16 acc[4] = {};
 #pragma unroll
-      for (int d = 0; d < kHeadDim; ++d) s = fmaf(qs[hh * kHeadDim + d], kf[d], s);
-      uint64_t key = ((uint64_t)order_key(s) << 32) | (uint32_t)(kBlock - 1 - tok);
+    for (int dc = 0; dc < 8; ++dc) {
+      float x[8] = {};
+      if (cok) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(qm + dc * 16);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(qm + dc * 16 + 4);
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)key, off);
-        const uint32_t hi = __shfl_xor((uint32_t)(key >> 32), off);
-        const uint64_t other = ((uint64_t)hi << 32) | lo;
-        key = other > key ? other : key;
+        for (int e = 0; e < 4; ++e) { x[e] = x0[e]; x[4 + e] = x1[e]; }
       }
-      if (lane == 0) best[w][hh] = key;
+      float r1[8], r2[8];
+      const bf16x8 hi = pack_bf16x8(x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r1[e] = x[e] - (float)hi[e];
+      const bf16x8 mid = pack_bf16x8(r1);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r2[e] = r1[e] - (float)mid[e];
+      const bf16x8 lo = pack_bf16x8(r2);
+      const int off = e0 ^ (dc << 4);
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        const bf16x8 kr = as_bf16x8(*reinterpret_cast<const u32x4*>(kt + rt * 32 * kHeadDim + off));
+        acc[rt] = mfma32(kr, hi, acc[rt]);
+        acc[rt] = mfma32(kr, mid, acc[rt]);
+        acc[rt] = mfma32(kr, lo, acc[rt]);
+      }
     }
-    block_sync();
-    if (tok < a.group) {
-      const uint64_t k0 = best[0][tok], k1 = best[1][tok];
-      const uint64_t k = k0 > k1 ? k0 : k1;
-      const int pos = kBlock - 1 - (int)(k & 0xffffffffu);
-      a.choice[(((int64_t)b * a.blocks + t) * a.blocks + j) * a.q_heads + g * a.group + tok] =
+    float best = -INFINITY;
+    int pos = 0;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float v = acc[rt][r];
+        if (v > best) {
+          best = v;
+          pos = rt * 32 + mfma32_row(r, lane);
+        }
+      }
+    }
+    const float ob = __shfl_xor(best, 32);
+    const int op = __shfl_xor(pos, 32);
+    if (ob > best || (ob == best && op < pos)) pos = op;
+    if (half == 0 && cok)
+      a.choice[(((int64_t)b * a.blocks + t) * a.blocks + j) * a.q_heads + g * a.group + hh] =
           (uint8_t)pos;
-    }
   }
 }
 
@@ -158,11 +190,10 @@ extern "C" int spx_rescue_choice(const float* qmean, const void* key_tiles, int 
   SPX_REQUIRE(batch > 0 && seq > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
               SPX_EINVAL, "bad shape: batch %d seq %d q_heads %d kv_heads %d", batch, seq, q_heads,
               kv_heads);
-  SPX_REQUIRE(q_heads / kv_heads <= kMaxGroup, SPX_EUNSUPPORTED,
-              "more than %d q heads per kv head", kMaxGroup);
   SPX_REQUIRE(qmean && key_tiles && choice, SPX_EINVAL, "null pointer");
-  SPX_REQUIRE((reinterpret_cast<uintptr_t>(key_tiles) & 15) == 0, SPX_EINVAL,
-              "key_tiles must be 16-byte aligned");
+  SPX_REQUIRE((reinterpret_cast<uintptr_t>(key_tiles) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(qmean) & 15) == 0,
+              SPX_EINVAL, "key_tiles and qmean must be 16-byte aligned");
   ChoiceArgs a{};
   a.qmean = qmean;
   a.kt = static_cast<const uint16_t*>(key_tiles);
@@ -171,6 +202,6 @@ extern "C" int spx_rescue_choice(const float* qmean, const void* key_tiles, int 
   a.group = q_heads / kv_heads;
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid(a.blocks, kv_heads, batch);
-  rescue_choice_kernel<<<grid, kBlock, 0, st>>>(a);
+  rescue_choice_kernel<<<grid, kChoiceThreads, 0, st>>>(a);
   return launch_status("rescue_choice");
 }

@@ -220,8 +220,10 @@ int spx_tile_mean_query(const void* q, const int64_t* q_strides, int batch, int 
                         int head_dim, int block_size, float* qmean, void* stream);
 
 /* Rescue token of every (query tile t, key block j < t, q head): the position p of
- * the block maximising qmean[t, h] . k[j, p] (fp32 dot products; the first position
- * on ties). qmean from spx_tile_mean_query; key_tiles from spx_block_pool.
+ * the block maximising qmean[t, h] . k[j, p] (dot products to fp32 accuracy: bf16
+ * keys times the fp32 means split exactly into three bf16 parts, on MFMA; the first
+ * position on ties). qmean (16-byte aligned) from spx_tile_mean_query; key_tiles from
+ * spx_block_pool.
  * choice: uint8 [B, NB, NB, Hq] contiguous, 0 where j >= t.
  * Replaces kernels.py:277-283 (token_scores / argmax inside rescue_tail). */
 int spx_rescue_choice(const float* qmean, const void* key_tiles, int batch, int seq, int q_heads,

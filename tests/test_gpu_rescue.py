@@ -20,7 +20,7 @@ def _choice(qg, kg, vg):
     return to_np(kernels.rescue_choice(qg, key_tiles))
 
 
-@pytest.mark.parametrize("length", (385, 1089))
+@pytest.mark.parametrize("length", (385, 1089, 4500))   # 4500: 245 columns for key block 0
 def test_rescue_choice_vs_oracle(gpu, length):
     """Same token as the float64 argmax, except fp32 near-ties (then the GPU's token
     scores within 1e-5 of the maximum)."""
