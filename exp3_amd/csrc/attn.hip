@@ -863,7 +863,9 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
                      int batch, int seq, int q_heads, int kv_heads, int head_dim,
                      int block_size, float scale, void* out, const int64_t* out_strides,
                      float* lse, const int64_t* lse_strides, void* stream) {
-  SPX_REQUIRE(head_dim == kHeadDim, SPX_EUNSUPPORTED, "head_dim %d unsupported (only 128)", head_dim);
+  SPX_REQUIRE(head_dim == kHeadDim || (head_dim == 256 && req.exact && !req.tail),
+              SPX_EUNSUPPORTED,
+              "head_dim %d unsupported (128; 256 for exact attention without a tail)", head_dim);
   SPX_REQUIRE(block_size == kBlock, SPX_EUNSUPPORTED, "block_size %d unsupported (only 128)", block_size);
   SPX_REQUIRE(batch > 0 && seq > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
               SPX_EINVAL, "bad shape: batch %d seq %d q_heads %d kv_heads %d", batch, seq,
@@ -900,6 +902,10 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
     SPX_REQUIRE(req.exact, SPX_EINVAL, "mean_tail needs index lists");
   }
   if (lse) SPX_REQUIRE(lse_strides != nullptr, SPX_EINVAL, "lse strides missing");
+  if (head_dim == 256)
+    return launch_attention_256(q, q_strides, key_tiles, value_tiles, indices, index_strides,
+                                counts, count_strides, batch, seq, q_heads, kv_heads, scale, out,
+                                out_strides, lse, lse_strides, stream);
 
   AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);

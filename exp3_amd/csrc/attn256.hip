@@ -1,0 +1,259 @@
+// Block-sparse causal flash attention at head_dim 256 (Qwen3.5 full-attention
+// layers, 16:4 GQA; check_qwen35_math.py; upstream/flashprefill_native_forward.py
+// :215-354 / :478-521 with D = 256, whose Triton launch walks each 128-token block
+// in four 32-key micro-tiles).
+//
+// gfx950 mapping
+//   * One workgroup per (query tile t, q head h): four waves of 32 query rows, one
+//     wave per SIMD. A wave keeps its Q rows in registers as MFMA B operands (16
+//     k-steps of 16 dims) and O^T (256 dims x 32 queries, eight 32 x 32 tiles) in
+//     the accumulators.
+//   * Keys stream in 32-key sub-blocks: the K rows (16 KB) and V^T (256 dims x 32
+//     key slots, 16 KB) of a sub-block are contiguous in the pool's d = 256 tiles and
+//     are copied verbatim into one of two LDS buffer pairs with direct global->LDS
+//     loads while the previous sub-block is computed (one barrier per sub-block).
+//   * Scores are formed transposed, S^T = K Q^T (v_mfma_f32_32x32x16_bf16, 16
+//     k-steps), so each lane owns one query column: the online softmax is in-lane
+//     plus one lane-half exchange, and the probabilities already sit in the B-operand
+//     layout of O^T += V^T P^T (key slot permutation of the value tiles). The running
+//     max moves only when it grows by more than 2^8 (lazy rescale).
+//   * The tile's list (entries outside [0, NB) skipped, as the reference's loop
+//     never reads them usefully) is compacted into LDS once; as in the reference,
+//     only the diagonal block j == t is masked (key > query).
+#include "common.h"
+
+namespace spx {
+
+constexpr int kD2 = 256;
+constexpr int kSub = 32;                   // keys per sub-block
+constexpr int kSubElems = kSub * kD2;      // 8192 bf16 = 16 KB
+constexpr int kA2Threads = 256;
+constexpr int kA2MaxBlocks = 1024;
+
+struct Attn256Args {
+  const uint16_t* q;
+  int64_t qs_b, qs_s, qs_h;
+  const uint16_t* kt;  // [B, Hkv, NB, 128, 256]: K rows, chunk c of row r at c ^ (r & 15)
+  const uint16_t* vt;  // [B, Hkv, NB, 4, 256, 32]: V^T per sub-block, chunk c of row d at c ^ ((d >> 2) & 3)
+  const int64_t* idx;  // [B, NB, NB, Hq] (strided) or null for every causal block
+  int64_t is_b, is_t, is_p, is_h;
+  const int32_t* cnt;
+  int64_t cs_b, cs_t, cs_h;
+  int batch, seq, q_heads, kv_heads, blocks;
+  float scale_log2;
+  uint16_t* out;
+  int64_t os_b, os_s, os_h;
+  float* lse;
+  int64_t ls_b, ls_s, ls_h;
+};
+
+// 16 KB from global memory into LDS: four instructions of 256 lanes x 16 bytes.
+__device__ __forceinline__ void dma_16k(const uint16_t* src, uint16_t* lds, int tid) {
+  const int w = tid >> 6;
+  const uint32_t lds_base =
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)lds;
+  const uint32_t voff = (uint32_t)tid * 16u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t m0 =
+        __builtin_amdgcn_readfirstlane(lds_base + (uint32_t)(i * kA2Threads + w * 64) * 16u);
+    const uint16_t* s = src + i * kA2Threads * 8;
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %2, %3\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(m0), "v"(voff), "s"(s)
+        : "memory");
+  }
+}
+
+__global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
+  const int per_tile = a.batch * a.q_heads;
+  const int t = a.blocks - 1 - (int)(blockIdx.x / per_tile);  // heaviest tiles first
+  const int bh = blockIdx.x % per_tile;
+  const int b = bh / a.q_heads, h = bh % a.q_heads;
+  const int g = h / (a.q_heads / a.kv_heads);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int col = lane & 31, half = lane >> 5;
+
+  __shared__ __align__(16) uint16_t kbuf[2][kSubElems];
+  __shared__ __align__(16) uint16_t vbuf[2][kSubElems];
+  __shared__ int list[kA2MaxBlocks];
+  __shared__ int list_len;
+
+  // compacted block list: ids in [0, NB), list order
+  if (w == 0) {
+    int n = a.idx ? a.cnt[b * a.cs_b + t * a.cs_t + h * a.cs_h] : t + 1;
+    n = max(0, min(n, a.blocks));
+    int base = 0;
+    for (int u0 = 0; u0 < n; u0 += 64) {
+      const int u = u0 + lane;
+      int j = -1;
+      if (u < n) j = a.idx ? (int)a.idx[b * a.is_b + t * a.is_t + u * a.is_p + h * a.is_h] : u;
+      const bool ok = j >= 0 && j < a.blocks;
+      const uint64_t m = __ballot(ok);
+      const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
+      if (ok) list[pos] = j;
+      base += __popcll(m);
+    }
+    if (lane == 0) list_len = base;
+  }
+  block_sync();
+  const int steps = list_len * 4;
+  const int64_t kv_block0 = ((int64_t)b * a.kv_heads + g) * a.blocks;
+
+  auto issue = [&](int s, int buf) {
+    const int j = __builtin_amdgcn_readfirstlane(list[s >> 2]);
+    const int sb = s & 3;
+    dma_16k(a.kt + ((kv_block0 + j) * kBlock + sb * kSub) * kD2, kbuf[buf], tid);
+    dma_16k(a.vt + (kv_block0 + j) * (kBlock * kD2) + sb * kSubElems, vbuf[buf], tid);
+  };
+  if (steps > 0) issue(0, 0);
+
+  const int qr = w * 32 + col;  // query row within the tile
+  const int64_t qrow = (int64_t)t * kBlock + qr;
+  const bool row_ok = qrow < a.seq;
+  bf16x8 qb[16];
+  {
+    const uint16_t* src = a.q + b * a.qs_b + qrow * a.qs_s + h * a.qs_h + half * 8;
+#pragma unroll
+    for (int dc = 0; dc < 16; ++dc) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (row_ok) raw = *reinterpret_cast<const u32x4*>(src + dc * 16);
+      asm volatile("" : "+v"(raw));  // consume now: its wait stays outside the loop
+      qb[dc] = as_bf16x8(raw);
+    }
+  }
+
+  // K operand: row col, 16-byte chunk 2 dc + half at ((2 dc + half) ^ (col & 15)):
+  // (dc >> 3) * 128 + (e0 ^ ((dc & 7) << 4)) elements past the row start.
+  const int e0 = (((col >> 1) & 7) << 4) + ((half ^ (col & 1)) << 3);
+  // V^T operand: dim row 32 dt + col, chunk 2 ks + half at ((2 ks + half) ^ ((col >> 2) & 3))
+  const int vsw = (col >> 2) & 3;
+
+  f32x16 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x16{};
+  float m_used = -INFINITY;  // log2 units; equal in both lane halves (same query)
+  float l = 0.0f;            // this half's share of the probability sum
+
+  for (int s = 0; s < steps; ++s) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    block_sync();  // sub-block s landed everywhere; buffers (s + 1) & 1 are free
+    if (s + 1 < steps) issue(s + 1, (s + 1) & 1);
+    const int j = __builtin_amdgcn_readfirstlane(list[s >> 2]);
+    const int sb = s & 3;
+    const uint16_t* kb = kbuf[s & 1] + col * kD2;
+    const uint16_t* vb = vbuf[s & 1];
+
+    f32x16 sc = {};
+#pragma unroll
+    for (int dc = 0; dc < 16; ++dc) {
+      const bf16x8 kr = as_bf16x8(*reinterpret_cast<const u32x4*>(kb + (dc >> 3) * 128 +
+                                                                      (e0 ^ ((dc & 7) << 4))));
+      sc = mfma32(kr, qb[dc], sc);
+    }
+
+    float x[16];
+    float mx = -INFINITY;
+    const bool diag = j == t;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = sb * kSub + mfma32_row(r, lane);
+      float v = sc[r] * a.scale_log2;
+      if (diag && key > qr) v = -INFINITY;
+      x[r] = v;
+      mx = fmaxf(mx, v);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (mx > m_used + 8.0f) {  // lazy rescale: only when the max grows by more than 2^8
+      const float f = exp2_fast(m_used - mx);  // 0 on the first sub-block
+      l *= f;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] *= f;
+      m_used = mx;
+    }
+    const float mref = m_used == -INFINITY ? 0.0f : m_used;
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      p[r] = exp2_fast(x[r] - mref);
+      l += p[r];
+    }
+    u32x4 pb0, pb1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      pb0[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
+      pb1[e] = pack_bf16x2(p[8 + 2 * e], p[8 + 2 * e + 1]);
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint16_t* vrow = vb + (dt * 32 + col) * kSub;
+      const bf16x8 v0 = as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + ((half ^ vsw) << 3)));
+      const bf16x8 v1 =
+          as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + (((2 + half) ^ vsw) << 3)));
+      o[dt] = mfma32(v0, as_bf16x8(pb0), o[dt]);
+      o[dt] = mfma32(v1, as_bf16x8(pb1), o[dt]);
+    }
+  }
+
+  l += __shfl_xor(l, 32);
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  if (row_ok) {
+    uint16_t* dst = a.out + b * a.os_b + qrow * a.os_s + h * a.os_h + 4 * half;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) {
+        const int r = 4 * grp;
+        u32x2 v;
+        v[0] = pack_bf16x2(o[dt][r] * inv, o[dt][r + 1] * inv);
+        v[1] = pack_bf16x2(o[dt][r + 2] * inv, o[dt][r + 3] * inv);
+        *reinterpret_cast<u32x2*>(dst + dt * 32 + 8 * grp) = v;
+      }
+    }
+    if (a.lse && half == 0)
+      a.lse[b * a.ls_b + qrow * a.ls_s + h * a.ls_h] =
+          l > 0.0f ? (m_used + log2f(l)) * kLn2 : -INFINITY;
+  }
+}
+
+int launch_attention_256(const void* q, const int64_t* q_strides, const void* key_tiles,
+                         const void* value_tiles, const int64_t* indices,
+                         const int64_t* index_strides, const int32_t* counts,
+                         const int64_t* count_strides, int batch, int seq, int q_heads,
+                         int kv_heads, float scale, void* out, const int64_t* out_strides,
+                         float* lse, const int64_t* lse_strides, void* stream) {
+  const int blocks = num_blocks(seq);
+  SPX_REQUIRE(blocks <= kA2MaxBlocks, SPX_EUNSUPPORTED, "seq %d exceeds %d blocks", seq,
+              kA2MaxBlocks);
+  Attn256Args a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.qs_b = q_strides[0]; a.qs_s = q_strides[1]; a.qs_h = q_strides[2];
+  a.kt = static_cast<const uint16_t*>(key_tiles);
+  a.vt = static_cast<const uint16_t*>(value_tiles);
+  a.idx = indices;
+  if (indices) {
+    a.is_b = index_strides[0]; a.is_t = index_strides[1]; a.is_p = index_strides[2];
+    a.is_h = index_strides[3];
+    a.cnt = counts;
+    a.cs_b = count_strides[0]; a.cs_t = count_strides[1]; a.cs_h = count_strides[2];
+  }
+  a.batch = batch; a.seq = seq; a.q_heads = q_heads; a.kv_heads = kv_heads; a.blocks = blocks;
+  a.scale_log2 = (float)((double)scale * 1.4426950408889634);
+  a.out = static_cast<uint16_t*>(out);
+  a.os_b = out_strides[0]; a.os_s = out_strides[1]; a.os_h = out_strides[2];
+  a.lse = lse;
+  if (lse) { a.ls_b = lse_strides[0]; a.ls_s = lse_strides[1]; a.ls_h = lse_strides[2]; }
+  const unsigned grid = (unsigned)(blocks * batch * q_heads);
+  attn256_kernel<<<grid, kA2Threads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return launch_status("attention_d256");
+}
+
+}  // namespace spx

@@ -117,6 +117,14 @@ __host__ __device__ __forceinline__ int value_slot_of_key(int key) {
 namespace spx {
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);
+// Exact attention at head_dim 256 (attn256.hip); arguments as spx_exact_attention,
+// already validated by the caller.
+int launch_attention_256(const void* q, const int64_t* q_strides, const void* key_tiles,
+                         const void* value_tiles, const int64_t* indices,
+                         const int64_t* index_strides, const int32_t* counts,
+                         const int64_t* count_strides, int batch, int seq, int q_heads,
+                         int kv_heads, float scale, void* out, const int64_t* out_strides,
+                         float* lse, const int64_t* lse_strides, void* stream);
 }  // namespace spx
 
 #define SPX_REQUIRE(cond, code, ...)        \

@@ -11,9 +11,14 @@
 //     position c ^ (r & 15). The attention kernel copies a tile into LDS verbatim
 //     (direct global->LDS loads) and reads MFMA operands bank-conflict free.
 //
-// Bandwidth-bound: each workgroup streams a 128 x 128 bf16 K tile and V tile with
-// 16-byte loads (each row is 256 contiguous bytes), reduces columns in registers,
+// Bandwidth-bound: each workgroup streams a 128 x D bf16 K tile and V tile with
+// 16-byte loads (each row is 2 D contiguous bytes), reduces columns in registers,
 // across lanes and across the four waves through LDS.
+//
+// Head dim 256 (Qwen3.5 full-attention layers): the same pass; key tiles keep the
+// [128 keys][256 dims] layout (chunk c of row r at c ^ (r & 15), c < 32), value tiles
+// are four 32-key sub-blocks [256 dims][32 slots] (16 KB each, the d = 256 attention
+// kernel's LDS image) with 16-byte chunk c of dim row d at c ^ ((d >> 2) & 3).
 #include "common.h"
 
 namespace spx {
@@ -35,7 +40,6 @@ struct PoolArgs {
 };
 
 constexpr int kPoolThreads = 256;
-constexpr int kVPitch = kBlock + 2;  // LDS row pitch (bf16) of the staged V tile
 
 __device__ __forceinline__ void accumulate8(const u32x4& raw, float* sum, float* sq) {
 #pragma unroll
@@ -49,39 +53,43 @@ __device__ __forceinline__ void accumulate8(const u32x4& raw, float* sum, float*
   }
 }
 
-// Sum a per-lane array of 8 floats over the 4 row groups of a wave (lanes that
-// differ in bits 4 and 5).
+// Sum a per-lane array of 8 floats over the row groups of a wave: lanes that differ
+// in bits 4 and 5 (D = 128: 16 chunks per row) or in bit 5 (D = 256: 32 chunks).
+template <int D>
 __device__ __forceinline__ void reduce_row_groups(float* x) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    x[e] += __shfl_xor(x[e], 16);
+    if (D == 128) x[e] += __shfl_xor(x[e], 16);
     x[e] += __shfl_xor(x[e], 32);
   }
 }
 
-template <bool DO_K, bool DO_V, bool DO_TILES>
+template <int D, bool DO_K, bool DO_V, bool DO_TILES>
 __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
+  constexpr int kChunks = D / 8;                    // 16-byte chunks per row
+  constexpr int kRowsPer = kBlock * kChunks / kPoolThreads;  // rows per row group
+  constexpr int kVPitch = D + 2;                    // LDS row pitch (bf16) of staged V
   const int j = blockIdx.x;
   const int b = blockIdx.y / a.kv_heads;
   const int g = blockIdx.y % a.kv_heads;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int c = tid & 15;        // 8-dim chunk
-  const int rg = tid >> 4;       // row group: rows rg * 8 + i
+  const int c = tid & (kChunks - 1);  // 8-dim chunk
+  const int rg = tid / kChunks;       // row group: rows rg * kRowsPer + i
   const int n = min(kBlock, a.seq - j * kBlock);
 
-  __shared__ float part[4][4][kHeadDim];                   // [quantity][wave][dim]
+  __shared__ float part[4][4][D];                          // [quantity][wave][dim]
   __shared__ __align__(16) uint16_t vrows[kBlock * kVPitch];  // staged V rows
-  __shared__ float sig_part[2];
+  __shared__ float sig_part[D / 64];
 
   float sk[8] = {}, qk[8] = {}, sv[8] = {}, qv[8] = {};
   const uint16_t* kbase = a.k + b * a.ks_b + g * a.ks_h + (int64_t)c * 8;
   const uint16_t* vbase = a.v + b * a.vs_b + g * a.vs_h + (int64_t)c * 8;
-  const int64_t tile_off = ((((int64_t)b * a.kv_heads + g) * a.blocks + j) * kBlock) * kHeadDim;
+  const int64_t tile_off = ((((int64_t)b * a.kv_heads + g) * a.blocks + j) * kBlock) * D;
 
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int row = rg * 8 + i;
+  for (int i = 0; i < kRowsPer; ++i) {
+    const int row = rg * kRowsPer + i;
     const bool valid = row < n;
     const int64_t token = (int64_t)j * kBlock + row;
     if (DO_K || DO_TILES) {
@@ -89,7 +97,7 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
       if (valid) raw = *reinterpret_cast<const u32x4*>(kbase + token * a.ks_s);
       if (DO_K && valid) accumulate8(raw, sk, qk);
       if (DO_TILES)
-        *reinterpret_cast<u32x4*>(a.key_tiles + tile_off + row * kHeadDim + ((c ^ (row & 15)) << 3)) = raw;
+        *reinterpret_cast<u32x4*>(a.key_tiles + tile_off + row * D + ((c ^ (row & 15)) << 3)) = raw;
     }
     if (DO_V || DO_TILES) {
       u32x4 raw = {0u, 0u, 0u, 0u};
@@ -103,9 +111,9 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
     }
   }
 
-  if (DO_K) { reduce_row_groups(sk); reduce_row_groups(qk); }
-  if (DO_V) { reduce_row_groups(sv); reduce_row_groups(qv); }
-  if (lane < 16) {
+  if (DO_K) { reduce_row_groups<D>(sk); reduce_row_groups<D>(qk); }
+  if (DO_V) { reduce_row_groups<D>(sv); reduce_row_groups<D>(qv); }
+  if (lane < kChunks) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int d = c * 8 + e;
@@ -115,10 +123,10 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
   }
   block_sync();
 
-  if (tid < kHeadDim) {
+  if (tid < D) {
     const int d = tid;
     const float count = (float)n;
-    const int64_t o = (((int64_t)b * a.blocks + j) * a.kv_heads + g) * kHeadDim + d;
+    const int64_t o = (((int64_t)b * a.blocks + j) * a.kv_heads + g) * D + d;
     if (DO_K) {
       const float s = part[0][0][d] + part[0][1][d] + part[0][2][d] + part[0][3][d];
       const float s2 = part[1][0][d] + part[1][1][d] + part[1][2][d] + part[1][3][d];
@@ -142,13 +150,14 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
   if (a.counts && blockIdx.y == 0 && tid == 0) a.counts[j] = n;
 
   if (DO_TILES) {
-    // Transposed write-out: thread -> (dim row d, 8-slot chunk); each gathers the
+    // Transposed write-out: thread -> (dim row d, 8-slot chunk gc); each gathers the
     // 8 keys of its slots from the staged rows and stores 16 bytes at the swizzled
-    // chunk position.
+    // chunk position (D = 128: [dim][128 slots], chunk gc ^ (d & 15); D = 256: sub-block
+    // gc / 4 of [dim][32 slots], chunk (gc & 3) ^ ((d >> 2) & 3)).
     uint16_t* tile = a.value_tiles + tile_off;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int id = tid + kPoolThreads * i;  // 0 .. 2047
+    for (int i = 0; i < 16 * D / kPoolThreads; ++i) {
+      const int id = tid + kPoolThreads * i;  // 0 .. 16 D - 1
       const int d = id >> 4;                  // dim row of the tile
       const int chunk = id & 15;              // slots chunk * 8 .. chunk * 8 + 7
       uint32_t w[4];
@@ -162,20 +171,42 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
         const uint32_t hi = vrows[(key0 + 1) * kVPitch + d];
         w[m >> 1] = lo | (hi << 16);
       }
-      *reinterpret_cast<u32x4*>(tile + d * kBlock + ((chunk ^ (d & 15)) << 3)) =
-          u32x4{w[0], w[1], w[2], w[3]};
+      uint16_t* dst;
+      if (D == 128)
+        dst = tile + d * kBlock + ((chunk ^ (d & 15)) << 3);
+      else
+        dst = tile + (chunk >> 2) * (D * 32) + d * 32 + (((chunk & 3) ^ ((d >> 2) & 3)) << 3);
+      *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
     }
   }
   if (DO_V) {
     block_sync();
-    if (a.sigma_v && tid == 0)
-      a.sigma_v[((int64_t)b * a.blocks + j) * a.kv_heads + g] = sqrtf(sig_part[0] + sig_part[1]);
+    if (a.sigma_v && tid == 0) {
+      float total = 0.0f;
+#pragma unroll
+      for (int x = 0; x < D / 64; ++x) total += sig_part[x];
+      a.sigma_v[((int64_t)b * a.blocks + j) * a.kv_heads + g] = sqrtf(total);
+    }
   }
 }
 
 }  // namespace spx
 
 using namespace spx;
+
+template <int D>
+static void launch_pool(int variant, dim3 grid, hipStream_t st, const PoolArgs& a) {
+  switch (variant) {
+    case 0: pool_kernel<D, false, false, false><<<grid, kPoolThreads, 0, st>>>(a); break;
+    case 1: pool_kernel<D, false, false, true><<<grid, kPoolThreads, 0, st>>>(a); break;
+    case 2: pool_kernel<D, false, true, false><<<grid, kPoolThreads, 0, st>>>(a); break;
+    case 3: pool_kernel<D, false, true, true><<<grid, kPoolThreads, 0, st>>>(a); break;
+    case 4: pool_kernel<D, true, false, false><<<grid, kPoolThreads, 0, st>>>(a); break;
+    case 5: pool_kernel<D, true, false, true><<<grid, kPoolThreads, 0, st>>>(a); break;
+    case 6: pool_kernel<D, true, true, false><<<grid, kPoolThreads, 0, st>>>(a); break;
+    default: pool_kernel<D, true, true, true><<<grid, kPoolThreads, 0, st>>>(a); break;
+  }
+}
 
 static int check_tensor4(const char* name, const void* p, const int64_t* st) {
   SPX_REQUIRE(p != nullptr && st != nullptr, SPX_EINVAL, "%s: null pointer", name);
@@ -192,7 +223,8 @@ extern "C" int spx_block_pool(const void* k, const int64_t* k_strides, const voi
                               int head_dim, int block_size, void* mean_k_bf16, float* mean_k,
                               float* mean_v, float* var_k, float* sigma_v, int32_t* counts,
                               void* key_tiles, void* value_tiles, void* stream) {
-  SPX_REQUIRE(head_dim == kHeadDim, SPX_EUNSUPPORTED, "head_dim %d unsupported (only 128)", head_dim);
+  SPX_REQUIRE(head_dim == 128 || head_dim == 256, SPX_EUNSUPPORTED,
+              "head_dim %d unsupported (128 or 256)", head_dim);
   SPX_REQUIRE(block_size == kBlock, SPX_EUNSUPPORTED, "block_size %d unsupported (only 128)", block_size);
   SPX_REQUIRE(batch > 0 && seq > 0 && kv_heads > 0, SPX_EINVAL,
               "batch, seq and kv_heads must be positive (got %d, %d, %d)", batch, seq, kv_heads);
@@ -223,16 +255,8 @@ extern "C" int spx_block_pool(const void* k, const int64_t* k_strides, const voi
   dim3 grid(a.blocks, batch * kv_heads);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int variant = (do_k ? 4 : 0) | (do_v ? 2 : 0) | (do_tiles ? 1 : 0);
-  switch (variant) {
-    case 0: pool_kernel<false, false, false><<<grid, kPoolThreads, 0, st>>>(a); break;
-    case 1: pool_kernel<false, false, true><<<grid, kPoolThreads, 0, st>>>(a); break;
-    case 2: pool_kernel<false, true, false><<<grid, kPoolThreads, 0, st>>>(a); break;
-    case 3: pool_kernel<false, true, true><<<grid, kPoolThreads, 0, st>>>(a); break;
-    case 4: pool_kernel<true, false, false><<<grid, kPoolThreads, 0, st>>>(a); break;
-    case 5: pool_kernel<true, false, true><<<grid, kPoolThreads, 0, st>>>(a); break;
-    case 6: pool_kernel<true, true, false><<<grid, kPoolThreads, 0, st>>>(a); break;
-    default: pool_kernel<true, true, true><<<grid, kPoolThreads, 0, st>>>(a); break;
-  }
+  if (head_dim == 128) launch_pool<128>(variant, grid, st, a);
+  else launch_pool<256>(variant, grid, st, a);
   return launch_status("block_pool");
 }
 

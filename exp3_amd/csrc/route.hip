@@ -148,7 +148,9 @@ struct V1Args {
   uint8_t* mask;
 };
 
+template <int D>
 __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
+  constexpr int kSteps = D / 16;  // 16-dim MFMA k-steps
   const int per_tile = a.batch * a.q_heads;
   const int t = a.blocks - 1 - blockIdx.x / per_tile;  // heaviest tiles first
   const int bh = blockIdx.x % per_tile;
@@ -167,12 +169,12 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   // Q rows as A operands: lane holds row (wave * 32 + col), dims dc*16 + 8*half + 0..7.
   const int row_in_tile = wave * 32 + col;
   const int64_t qrow = (int64_t)t * kBlock + row_in_tile;
-  bf16x8 qa[8];
+  bf16x8 qa[kSteps];
   {
     const uint16_t* src = a.q + b * a.qs_b + qrow * a.qs_s + h * a.qs_h + half * 8;
     const bool ok = qrow < a.seq;
 #pragma unroll
-    for (int dc = 0; dc < 8; ++dc) {
+    for (int dc = 0; dc < kSteps; ++dc) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (ok) raw = *reinterpret_cast<const u32x4*>(src + dc * 16);
       qa[dc] = as_bf16x8(raw);
@@ -185,16 +187,16 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
     const int j = jc * 32 + col;  // this lane's block column
     f32x16 acc = {};
     {
-      bf16x8 kb[8];
+      bf16x8 kb[kSteps];
       const bool ok = j < a.blocks;
 #pragma unroll
-      for (int dc = 0; dc < 8; ++dc) {
+      for (int dc = 0; dc < kSteps; ++dc) {
         u32x4 raw = {0u, 0u, 0u, 0u};
         if (ok) raw = *reinterpret_cast<const u32x4*>(kb_base + (int64_t)j * a.ms_j + dc * 16);
         kb[dc] = as_bf16x8(raw);
       }
 #pragma unroll
-      for (int dc = 0; dc < 8; ++dc) acc = mfma32(qa[dc], kb[dc], acc);
+      for (int dc = 0; dc < kSteps; ++dc) acc = mfma32(qa[dc], kb[dc], acc);
     }
     // acc[r] = S[row 8*(r/4) + 4*half + r%4 of this wave][block j]
     const int64_t key_end = (int64_t)(j + 1) * kBlock - 1;
@@ -385,7 +387,8 @@ static int check_q(const char* name, const void* p, const int64_t* st) {
 static int v1_common(const void* q, const int64_t* q_strides, const void* mean_k,
                      const int64_t* mk_strides, int batch, int seq, int q_heads, int kv_heads,
                      int head_dim, int block_size, float scale, V1Args* a) {
-  SPX_REQUIRE(head_dim == kHeadDim, SPX_EUNSUPPORTED, "head_dim %d unsupported (only 128)", head_dim);
+  SPX_REQUIRE(head_dim == 128 || head_dim == 256, SPX_EUNSUPPORTED,
+              "head_dim %d unsupported (128 or 256)", head_dim);
   SPX_REQUIRE(block_size == kBlock, SPX_EUNSUPPORTED, "block_size %d unsupported (only 128)", block_size);
   SPX_REQUIRE(batch > 0 && seq > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
               SPX_EINVAL, "bad shape: batch %d seq %d q_heads %d kv_heads %d", batch, seq,
@@ -419,7 +422,10 @@ extern "C" int spx_v1_scores(const void* q, const int64_t* q_strides, const void
   a.ss_b = score_strides[0]; a.ss_t = score_strides[1]; a.ss_j = score_strides[2];
   a.ss_h = score_strides[3];
   const int grid = a.blocks * batch * q_heads;
-  v1_route_kernel<<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  if (head_dim == 128)
+    v1_route_kernel<128><<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  else
+    v1_route_kernel<256><<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
   return launch_status("v1_scores");
 }
 
@@ -448,7 +454,10 @@ extern "C" int spx_v1_route(const void* q, const int64_t* q_strides, const void*
   a.counts = counts;
   a.mask = mask;
   const int grid = a.blocks * batch * q_heads;
-  v1_route_kernel<<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  if (head_dim == 128)
+    v1_route_kernel<128><<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  else
+    v1_route_kernel<256><<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
   return launch_status("v1_route");
 }
 

@@ -8,6 +8,11 @@
   python -m exp3_amd.sweeps long [--seq 131072] [--needles 256]
       long context: cgf_mean and dispersion_mean at alpha 0.04 (plus mean_native
       at 0.04 for reference), same columns
+  python -m exp3_amd.sweeps d256 [--seq 32640]
+      head_dim 256 with 16 query / 4 KV heads (Qwen3.5 full-attention layer shape,
+      check_qwen35_math.py): dense (torch SDPA and the HIP kernel) and fp_v1 at
+      alpha 0.08; ms/layer, the attention kernel's HIP-event time and its rate over
+      the selected 128 x 128 tiles (4 x 128 x 128 x 256 FLOP each)
   python -m exp3_amd.sweeps model [--seq 32640] [--layers 28] [--repeats 3]
       full prefill of a random-init Qwen2.5-7B-shaped model built from a local
       config (28 layers, hidden 3584, FFN 18944, 28/4 heads, RMSNorm 1e-6,
@@ -37,21 +42,27 @@ class _Layer:
     layer_idx = 0
 
 
-def _layer_case(torch, attention, kernels, q, k, v, method, alpha, steps=5, warmup=2):
-    scale = q.shape[-1] ** -0.5
-    backend = attention.AttentionBackend(alpha=alpha, register=False)
+def _layer_case(torch, attention, kernels, q, k, v, method, alpha, steps=5, warmup=2,
+                dense_impl="sdpa", scale=None):
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    backend = attention.AttentionBackend(alpha=alpha, register=False, dense_impl=dense_impl)
     backend.configure(method, alpha)
+    backend.kernel_events = []
     qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
     for _ in range(warmup):
         backend.forward(_Layer(), qt, kt, vt, None, scale)
     torch.cuda.synchronize()
+    backend.kernel_events.clear()
     t0 = time.perf_counter()
     for _ in range(steps):
         backend.forward(_Layer(), qt, kt, vt, None, scale)
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1000.0 / steps
-    seq, heads = q.shape[1], q.shape[2]
+    kernel_ms = (sum(x.elapsed_time(y) for x, y in backend.kernel_events)
+                 / len(backend.kernel_events)) if backend.kernel_events else None
+    seq, heads, dim = q.shape[1], q.shape[2], q.shape[3]
     blocks = math.ceil(seq / 128)
+    selected_tiles = heads * blocks * (blocks + 1) // 2
     if method == "dense":
         density, pair_ratio = 1.0, 1.0
     else:
@@ -61,11 +72,17 @@ def _layer_case(torch, attention, kernels, q, k, v, method, alpha, steps=5, warm
         else:
             _, _, _, cnt, sel = backend._new_selection(q, k, v, scale, record)
         acct = kernels.selection_accounting(sel, seq, 128, 128, method, 32)
-        density = float(cnt.sum().item()) / (heads * blocks * (blocks + 1) / 2)
+        selected_tiles = int(cnt.sum().item())
+        density = selected_tiles / (heads * blocks * (blocks + 1) / 2)
         pair_ratio = float(acct["effective_exact_token_pair_ratio"].item())
-    return {"method": method, "alpha": alpha if method != "dense" else None, "seq": seq,
-            "ms_per_layer": round(ms, 3), "block_density": round(density, 5),
-            "exact_pair_ratio": round(pair_ratio, 5)}
+    row = {"method": method, "alpha": alpha if method != "dense" else None, "seq": seq,
+           "ms_per_layer": round(ms, 3), "block_density": round(density, 5),
+           "exact_pair_ratio": round(pair_ratio, 5)}
+    if kernel_ms:
+        flops = 4.0 * 128 * 128 * dim * selected_tiles
+        row.update({"kernel_ms": round(kernel_ms, 3),
+                    "kernel_tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 1)})
+    return row
 
 
 def run_layer_sweep(seq, needles, seed, cases, label):
@@ -76,6 +93,21 @@ def run_layer_sweep(seq, needles, seed, cases, label):
     for method, alpha in cases:
         row = _layer_case(torch, attention, kernels, q, k, v, method, alpha)
         row.update({"sweep": label, "needles": needles, "seed": seed})
+        print(json.dumps(row), flush=True)
+
+
+def run_d256(seq, seed):
+    import torch
+    from exp3_amd import _lib, attention, kernels, synthetic
+    _lib.load()
+    q, k, v, _ = synthetic.make_inputs(seq, seed=seed, q_heads=16, kv_heads=4, head_dim=256,
+                                       device="cuda")
+    cases = [("dense", "sdpa"), ("dense", "hip"), ("fp_v1", "sdpa")]
+    for method, dense_impl in cases:
+        row = _layer_case(torch, attention, kernels, q, k, v, method, 0.08, steps=5, warmup=2,
+                          dense_impl=dense_impl, scale=256 ** -0.5)
+        row.update({"sweep": "d256", "q_heads": 16, "kv_heads": 4, "head_dim": 256,
+                    "impl": dense_impl if method == "dense" else "hip"})
         print(json.dumps(row), flush=True)
 
 
@@ -157,6 +189,9 @@ def main(argv=None) -> int:
     lo.add_argument("--seq", type=int, default=131072)
     lo.add_argument("--needles", type=int, default=256)
     lo.add_argument("--seed", type=int, default=17)
+    d2 = sub.add_parser("d256")
+    d2.add_argument("--seq", type=int, default=32640)
+    d2.add_argument("--seed", type=int, default=17)
     mo = sub.add_parser("model")
     mo.add_argument("--seq", type=int, default=32640)
     mo.add_argument("--layers", type=int, default=28)
@@ -170,6 +205,8 @@ def main(argv=None) -> int:
         cases = [(m, a) for a in (0.04, 0.08, 0.16) for m in MEAN_FOUR]
         cases += [("fp_v1", 0.08), ("dense", 0.08)]
         run_layer_sweep(args.seq, args.needles, args.seed, cases, "needles")
+    elif args.cmd == "d256":
+        run_d256(args.seq, args.seed)
     elif args.cmd == "long":
         cases = [("cgf_mean", 0.04), ("dispersion_mean", 0.04), ("mean_native", 0.04)]
         run_layer_sweep(args.seq, args.needles, args.seed, cases, "long")

@@ -90,7 +90,8 @@ def deal_output_score(score: torch.Tensor, attention_sink: int, window: int,
 def attention_tiles(k: torch.Tensor, v: torch.Tensor, block_size: int = 128):
     """Per-block K and V tiles the attention kernel copies into LDS verbatim:
     key tiles ``[B, Hkv, NB, 128, D]`` and value tiles ``[B, Hkv, NB, D, 128]``
-    (V transposed, keys permuted), zero past the sequence end, 16-byte chunks
+    (V transposed, keys permuted; at D = 256 four 32-key sub-blocks
+    ``[256, 32]`` per block), zero past the sequence end, 16-byte chunks
     XOR-swizzled by row; produced by the pooling pass."""
     device = _lib.require_gpu(k, v)
     k = _lib.kernel_view(k)

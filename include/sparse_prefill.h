@@ -18,8 +18,11 @@
  *   - Score / mask / index tensors use [batch, query_block, key_block, head].
  *     Outputs documented as "contiguous" must be densely packed in that order.
  *   - bf16 tensors are raw 16-bit bf16 bit patterns; masks are uint8 (0 / 1).
- *   - head_dim must be 128 and block_size 128 (the Qwen2.5-7B routing shape);
- *     q_heads must be a multiple of kv_heads.
+ *   - block_size must be 128 and head_dim 128 (the Qwen2.5-7B routing shape);
+ *     spx_block_pool / spx_block_mean_k / spx_block_descriptors, spx_v1_scores /
+ *     spx_v1_route and spx_exact_attention also take head_dim 256 (Qwen3.5
+ *     full-attention layers, check_qwen35_math.py). q_heads must be a multiple
+ *     of kv_heads.
  *   - Return 0 on success or a negative SPX_E* code; spx_last_error() then
  *     returns a thread-local message.
  */
@@ -70,10 +73,14 @@ int spx_block_descriptors(const void* k, const int64_t* k_strides, const void* v
  * attention tiles the attention entry points read. Null outputs are skipped;
  * key_tiles and value_tiles are produced together.
  * key_tiles:   [B, Hkv, NB, 128, D] bf16, the block's K rows;
- * value_tiles: [B, Hkv, NB, D, 128] bf16, V transposed per block with the key
- *              permutation documented in exp3_amd/csrc/common.h.
- * Rows / keys past seq are zero, and inside every 128 x 128 tile the 16-byte
- * chunk c of row r is stored at chunk position c ^ (r & 15) (the LDS layout).
+ * value_tiles: [B, Hkv, NB, D, 128] bf16 (D = 128), V transposed per block with
+ *              the key permutation documented in exp3_amd/csrc/common.h; for
+ *              D = 256 the same storage holds four 32-key sub-blocks
+ *              [256 dims][32 key slots] per block.
+ * Rows / keys past seq are zero. In a key tile the 16-byte chunk c of row r is
+ * stored at chunk position c ^ (r & 15) (c < D / 8); in a D = 128 value tile the
+ * same rule holds per dim row, in a D = 256 sub-block chunk c (< 4) of dim row d
+ * sits at c ^ ((d >> 2) & 3) (the attention kernels' LDS layouts).
  * Fuses kernels.py:22-46 with upstream/flashprefill_native_forward.py:420-442
  * (the descriptor stage of attention.py:80-86). */
 int spx_block_pool(const void* k, const int64_t* k_strides, const void* v,
@@ -159,7 +166,8 @@ int64_t spx_selector_workspace_bytes(int batch, int seq, int kv_heads, int head_
  * key_tiles / value_tiles come from spx_block_pool. indices: int64 [B, NB, NB, Hq] (strided),
  * counts: int32 [B, NB, Hq] (strided); indices == NULL selects every causal block
  * (dense causal attention). out: bf16 [B, S, Hq, D] (strided); lse: natural-log LSE
- * fp32 [B, S, Hq] (strided, may be NULL).
+ * fp32 [B, S, Hq] (strided, may be NULL). List ids outside [0, NB) are skipped;
+ * only the block equal to the query tile is masked (key > query). head_dim 128 or 256.
  * Replaces upstream/flashprefill_native_forward.py:478-521 (exact_attention) and the
  * Triton kernel _flash_forward (:215-354). */
 int spx_exact_attention(const void* q, const int64_t* q_strides, const void* key_tiles,
