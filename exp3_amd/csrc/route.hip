@@ -7,9 +7,11 @@
 //     S[row][j] = q_row . Kbar_j          (v_mfma_f32_32x32x16_bf16, fp32 acc)
 //     x = S * fp32(scale * log2 e)
 // Row i of tile t is valid for block j iff i >= 128 (j + 1) - 1 and i < S. Each
-// lane reduces its 16 rows of one block column to (max, sum 2^(x - max)), merges
-// with the other lane half and with the other waves through LDS, giving M_tj and
-// m_tj. The normalisation w_j = m_tj 2^(M_tj - max_j M_tj) / (sum_j w + 1e-9)
+// lane reduces its 16 rows of one block column to (max, sum 2^(x - max)) and
+// merges with the other lane half; every wave walks all chunks on its own (the
+// next chunk's Kbar operands load while the current one is reduced) and leaves its
+// rows' partials in LDS, and after one barrier the four waves' partials are merged
+// in a fixed order, giving M_tj and m_tj. The normalisation w_j = m_tj 2^(M_tj - max_j M_tj) / (sum_j w + 1e-9)
 // runs in the same workgroup, so the raw scores never reach HBM.
 //
 // Selection (upstream :357-407 and kernels.py:129-160) is one shared device
@@ -161,8 +163,8 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
 
   __shared__ float blk_max[kMaxBlocks];
   __shared__ float blk_mass[kMaxBlocks];
-  __shared__ float part_max[4][32];
-  __shared__ float part_mass[4][32];
+  __shared__ float part_max[4][kMaxBlocks];   // per-wave (max, mass) of every block
+  __shared__ float part_mass[4][kMaxBlocks];
   __shared__ float scratch[8];
   __shared__ int wave_counts[8];
 
@@ -181,19 +183,36 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
     }
   }
   const uint16_t* kb_base = a.kbar + b * a.ms_b + g * a.ms_h + half * 8;
+  auto load_kbar = [&](int jc, bf16x8 (&kb)[kSteps]) {
+    const int j = jc * 32 + col;
+    const bool ok = j < a.blocks;
+#pragma unroll
+    for (int dc = 0; dc < kSteps; ++dc) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (ok) raw = *reinterpret_cast<const u32x4*>(kb_base + (int64_t)j * a.ms_j + dc * 16);
+      kb[dc] = as_bf16x8(raw);
+    }
+  };
 
+  // Each wave walks every chunk of 32 blocks on its own (no barrier inside the
+  // loop; the next chunk's Kbar operands load while this one is reduced) and
+  // leaves its 32 rows' (max, mass) per block in LDS; the four waves merge after.
+  // (prefetch at D = 128 only: at D = 256 the second operand set costs occupancy)
+  constexpr bool kPrefetch = D == 128;
   const int nchunks = (t + 1 + 31) / 32;
+  bf16x8 kb_next[kSteps];
+  if (kPrefetch && nchunks > 0) load_kbar(0, kb_next);
   for (int jc = 0; jc < nchunks; ++jc) {
     const int j = jc * 32 + col;  // this lane's block column
     f32x16 acc = {};
     {
       bf16x8 kb[kSteps];
-      const bool ok = j < a.blocks;
+      if (kPrefetch) {
 #pragma unroll
-      for (int dc = 0; dc < kSteps; ++dc) {
-        u32x4 raw = {0u, 0u, 0u, 0u};
-        if (ok) raw = *reinterpret_cast<const u32x4*>(kb_base + (int64_t)j * a.ms_j + dc * 16);
-        kb[dc] = as_bf16x8(raw);
+        for (int dc = 0; dc < kSteps; ++dc) kb[dc] = kb_next[dc];
+        if (jc + 1 < nchunks) load_kbar(jc + 1, kb_next);
+      } else {
+        load_kbar(jc, kb);
       }
 #pragma unroll
       for (int dc = 0; dc < kSteps; ++dc) acc = mfma32(qa[dc], kb[dc], acc);
@@ -227,29 +246,26 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
       mx = nm;
       mass = merged;
     }
-    if (half == 0) {
-      part_max[wave][col] = mx;
-      part_mass[wave][col] = mass;
+    if (half == 0 && j < a.blocks) {
+      part_max[wave][j] = mx;
+      part_mass[wave][j] = mass;
     }
-    block_sync();
-    if (tid < 32) {
-      float m = part_max[0][tid];
-      for (int w = 1; w < 4; ++w) m = fmaxf(m, part_max[w][tid]);
-      float s = 0.0f;
-      if (m != -INFINITY) {
-        for (int w = 0; w < 4; ++w) {
-          const float pm = part_max[w][tid];
-          if (pm != -INFINITY) s += part_mass[w][tid] * exp2_fast(pm - m);
-        }
-      }
-      const int jj = jc * 32 + tid;
-      if (jj < a.blocks) {
-        blk_max[jj] = m;
-        blk_mass[jj] = s;
-      }
-    }
-    block_sync();
   }
+  block_sync();
+  for (int jj = tid; jj < min(nchunks * 32, a.blocks); jj += kRouteThreads) {
+    float m = part_max[0][jj];
+    for (int w = 1; w < 4; ++w) m = fmaxf(m, part_max[w][jj]);
+    float s2 = 0.0f;
+    if (m != -INFINITY) {
+      for (int w = 0; w < 4; ++w) {
+        const float pm = part_max[w][jj];
+        if (pm != -INFINITY) s2 += part_mass[w][jj] * exp2_fast(pm - m);
+      }
+    }
+    blk_max[jj] = m;
+    blk_mass[jj] = s2;
+  }
+  block_sync();
 
   // normalize_scores over j <= t; j > t has M = -inf and contributes 0.
   float local = -INFINITY;
