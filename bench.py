@@ -20,7 +20,9 @@ Also reported on the same line:
                 the headline table plus fp_v1_rescue and fp_v1_rescue_v2);
   stages        per-stage kernel times with their roofline fractions;
   cpu_baseline  the CPU oracle (numpy restatement of the reference path) on a
-                bounded sample of the same workload, scaled to ms per layer.
+                bounded sample of the same workload, scaled to ms per layer; plus
+                BASELINE config 1 (S=4096) through the oracle in full beside the same
+                layer on the GPU (--cpu-all-methods: the 32K sample for every method).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -59,6 +61,8 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample-tiles", type=int, default=4, help="minimum sampled query tiles")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of sampled attention")
+    p.add_argument("--cpu-all-methods", action="store_true",
+                   help="also time the CPU oracle for every method (several minutes)")
     p.add_argument("--traffic-file", default=str(ROOT / "profiles" / "hbm_traffic.json"))
     return p.parse_args()
 
@@ -141,25 +145,82 @@ def achievable_peaks(torch):
     return {"gemm_bf16_16384_tflops": round(gemm, 1), "copy_1gib_gbs": round(copy, 1)}
 
 
+def _cpu_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+def _cpu_model():
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return cpu
+
+
+def _oracle_route(ref, qn, kn, vn, scale, method, alpha):
+    """The oracle's routing for ``method`` (attention_layer's first half):
+    (indices, counts, selected, descriptors, rescue choice)."""
+    import numpy as np
+    batch, seq, heads, _ = qn.shape
+    blocks = ref.num_blocks(seq)
+    desc = None
+    if method == "dense":
+        sel = np.broadcast_to(np.arange(blocks)[None, :, None, None]
+                              >= np.arange(blocks)[None, None, :, None], (batch, blocks, blocks, heads))
+        idx, cnt = ref.indices_from_mask(sel)
+    elif method in ref.V1_ROUTED:
+        if method == "mean_native":
+            desc = ref.block_descriptors(kn, vn, precision="f32")
+        kbar = ref.block_mean_k(kn, precision="f32")
+        scores = ref.v1_scores(qn, kbar, scale, precision="f32")
+        idx, cnt = ref.deal_output_score(scores, 2, 4, alpha, 2, 0)
+        sel = ref.mask_from_indices(idx, cnt)
+    else:
+        desc = ref.block_descriptors(kn, vn, precision="f32")
+        scores = ref.selector_scores(qn, desc, scale, method, precision="f32")
+        sel = ref.protected_selection(scores, alpha, 2, 4, 2)
+        idx, cnt = ref.indices_from_mask(sel)
+    choice = ref.rescue_choice(qn, kn, precision="f32") if method in ref.RESCUE_METHODS else None
+    return idx, cnt, sel, desc, choice
+
+
+def _oracle_tiles(ref, qn, kn, vn, scale, method, route, tiles):
+    """The oracle's attention part of the layer for the given query tiles (all
+    tiles for None); rows outside the tiles are left as the exact part's zeros."""
+    import numpy as np
+    idx, cnt, sel, desc, choice = route
+    out, lse = ref.exact_attention(qn, kn, vn, idx, cnt, scale, precision="f32", tiles=tiles)
+    if method in ref.MEAN_METHODS:
+        t_out, t_lse = ref.mean_tail(qn, desc, sel, scale, precision="f32", tiles=tiles)
+    elif method in ref.RESCUE_METHODS:
+        t_out, t_lse = ref.rescue_tail(qn, kn, vn, sel, scale, remainder=method == "fp_v1_rescue_v2",
+                                       precision="f32", tiles=tiles, choice=choice)
+    else:
+        return out
+    rows = slice(None) if tiles is None else np.concatenate(
+        [np.arange(t * 128, min(qn.shape[1], t * 128 + 128)) for t in tiles])
+    merged, _ = ref.merge_exact_mean(out[:, rows], lse[:, rows], t_out[:, rows], t_lse[:, rows])
+    out[:, rows] = merged
+    return out
+
+
 def cpu_baseline(q, k, v, scale, method, alpha, sample_tiles, budget_s):
     """Time the CPU oracle (reference semantics in numpy float32) on the full
     routing stages plus a sample of query tiles of the attention stages; scale
     the sampled part by selected-block work to a whole layer."""
     import numpy as np
     from oracle import reference_cpu as ref
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
     qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
     blocks = ref.num_blocks(qn.shape[1])
     t0 = time.perf_counter()
-    desc = ref.block_descriptors(kn, vn, precision="f32")
-    kbar = ref.block_mean_k(kn, precision="f32")
-    scores = ref.v1_scores(qn, kbar, scale, precision="f32")
-    idx, cnt = ref.deal_output_score(scores, 2, 4, alpha, 2, 0)
-    sel = ref.mask_from_indices(idx, cnt)
+    route = _oracle_route(ref, qn, kn, vn, scale, method, alpha)
     routing_s = time.perf_counter() - t0
     # query tiles in a stratified order (coarse to fine over the sequence) until the
     # time budget is spent, so the sample is spread over short and long tiles
@@ -173,37 +234,53 @@ def cpu_baseline(q, k, v, scale, method, alpha, sample_tiles, budget_s):
     tiles = []
     t1 = time.perf_counter()
     for t in order:
-        ex_out, ex_lse = ref.exact_attention(qn, kn, vn, idx, cnt, scale, precision="f32", tiles=[t])
-        m_out, m_lse = ref.mean_tail(qn, desc, sel, scale, precision="f32", tiles=[t])
-        rows = np.arange(t * 128, min(qn.shape[1], t * 128 + 128))
-        ref.merge_exact_mean(ex_out[:, rows], ex_lse[:, rows], m_out[:, rows], m_lse[:, rows])
+        _oracle_tiles(ref, qn, kn, vn, scale, method, route, [t])
         tiles.append(t)
         if len(tiles) >= sample_tiles and time.perf_counter() - t1 >= budget_s:
             break
     attention_s = time.perf_counter() - t1
-    work = cnt.sum(axis=(0, 2)).astype(np.float64) + 1.0   # per tile (+1: the mean-tail row pass)
+    work = route[1].sum(axis=(0, 2)).astype(np.float64) + 1.0   # per tile (+1: the tail row pass)
     scale_up = work.sum() / work[tiles].sum()
     total_ms = (routing_s + attention_s * scale_up) * 1000.0
-    cpu = platform.processor() or platform.machine()
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {
         "value": round(total_ms, 1),
         "unit": "ms",
-        "cores": int(threads),
+        "cores": int(_cpu_threads()),
         "kind": "port",
-        "sample": (f"{method} alpha={alpha} S={qn.shape[1]}: pooling, V1 scores and selection "
-                   f"over all {blocks} query tiles ({routing_s:.1f} s), exact attention + mean tail "
-                   f"+ merge over {len(tiles)} query tiles spread over the sequence ({attention_s:.1f} s) "
-                   f"scaled x{scale_up:.1f} by selected-block work; numpy float32 oracle "
-                   f"(reference's own harness pins 1 thread, evaluate.py:793)"),
-        "cpu": cpu,
+        "sample": (f"{method} alpha={alpha} S={qn.shape[1]}: routing over all {blocks} query tiles "
+                   f"({routing_s:.1f} s), attention (exact blocks + tail + merge) over {len(tiles)} "
+                   f"query tiles spread over the sequence ({attention_s:.1f} s) scaled x{scale_up:.1f} "
+                   f"by selected-block work; numpy float32 oracle (reference's own harness pins "
+                   f"1 thread, evaluate.py:793)"),
+        "cpu": _cpu_model(),
     }
+
+
+def cpu_config1(method, alpha, seed, torch):
+    """S=4096, the whole layer through the CPU oracle (no
+    sampling), beside the same layer on the GPU, with their max / mean abs
+    difference."""
+    import numpy as np
+    from oracle import reference_cpu as ref
+    from exp3_amd import attention, synthetic
+    q, k, v, _ = synthetic.make_inputs(4096, seed=seed)
+    scale = 128 ** -0.5
+    qn, kn, vn = (x.float().numpy() for x in (q, k, v))
+    t0 = time.perf_counter()
+    route = _oracle_route(ref, qn, kn, vn, scale, method, alpha)
+    expected = _oracle_tiles(ref, qn, kn, vn, scale, method, route, None)
+    cpu_ms = (time.perf_counter() - t0) * 1000.0
+    qg, kg, vg = q.cuda(), k.cuda(), v.cuda()
+    backend = attention.AttentionBackend(alpha=alpha, register=False)
+    backend.configure(method, alpha)
+    gpu_ms = timed_forward(backend, qg, kg, vg, scale, 10, 3, torch)
+    out, _ = backend.forward(Layer(), qg.transpose(1, 2), kg.transpose(1, 2), vg.transpose(1, 2),
+                             None, scale)
+    diff = np.abs(out.float().cpu().numpy() - expected)
+    return {"config": "BASELINE config 1", "method": method, "alpha": alpha, "seq": 4096,
+            "cpu_ms": round(cpu_ms, 1), "cpu_cores": int(_cpu_threads()), "kind": "port",
+            "gpu_ms": round(gpu_ms, 4), "max_abs_gpu_vs_cpu": float(diff.max()),
+            "mean_abs_gpu_vs_cpu": float(diff.mean())}
 
 
 def main():
@@ -280,6 +357,12 @@ def main():
     if not args.no_cpu_baseline:
         baseline = cpu_baseline(q, k, v, scale, args.method, args.alpha, args.cpu_sample_tiles,
                                 args.cpu_budget)
+        baseline["config1"] = cpu_config1(args.method, args.alpha, args.seed, torch)
+        if args.cpu_all_methods:
+            baseline["per_method"] = {
+                name: cpu_baseline(q, k, v, scale, name, args.alpha, args.cpu_sample_tiles,
+                                   args.cpu_budget)
+                for name in attention.METHODS}
 
     line = {
         "metric": "sparse-prefill attn ms/layer @32K Qwen2.5-7B shape",

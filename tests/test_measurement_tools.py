@@ -65,3 +65,22 @@ def test_qwen2_7b_config_matches_the_model_shape():
         model = transformers.Qwen2ForCausalLM(cfg)
     assert sum(p.numel() for p in model.parameters()) == 7_615_616_512   # Qwen2.5-7B
     assert model.model.layers[0].self_attn.q_proj.bias is not None       # QKV bias
+
+
+@pytest.mark.parametrize("method", ("dense", "fp_v1", "mean_native", "mean_balanced", "cgf_mean",
+                                    "dispersion_mean", "fp_v1_rescue", "fp_v1_rescue_v2"))
+def test_bench_cpu_baseline_layer_equals_oracle_layer(method):
+    """bench.py's CPU baseline splits the oracle layer into routing and per-tile
+    attention; the two halves over all tiles give exactly the oracle's layer."""
+    import numpy as np
+    import bench
+    from oracle import reference_cpu as ref
+    from tests.helpers import inputs, to_np, SCALE
+    q, k, v = inputs(385, seed=29)
+    qn, kn, vn = to_np(q), to_np(k), to_np(v)
+    route = bench._oracle_route(ref, qn, kn, vn, SCALE, method, 0.08)
+    out = bench._oracle_tiles(ref, qn, kn, vn, SCALE, method, route, None)
+    expected = ref.attention_layer(qn, kn, vn, SCALE, method, 0.08, precision="f32")
+    np.testing.assert_array_equal(out, expected["output"])
+    sampled = bench._oracle_tiles(ref, qn, kn, vn, SCALE, method, route, [1])
+    np.testing.assert_array_equal(sampled[:, 128:256], expected["output"][:, 128:256])
