@@ -150,12 +150,22 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
     const uint16_t* kb = kbuf[s & 1] + col * kD2;
     const uint16_t* vb = vbuf[s & 1];
 
+    // operand reads in groups of four k-steps (fenced), so that at most four K
+    // operands are live: with O (128) and Q (64) the wave stays under 256 VGPRs
+    // and O never leaves the registers it accumulates in
     f32x16 sc = {};
 #pragma unroll
-    for (int dc = 0; dc < 16; ++dc) {
-      const bf16x8 kr = as_bf16x8(*reinterpret_cast<const u32x4*>(kb + (dc >> 3) * 128 +
-                                                                      (e0 ^ ((dc & 7) << 4))));
-      sc = mfma32(kr, qb[dc], sc);
+    for (int g4 = 0; g4 < 4; ++g4) {
+      bf16x8 kr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int dc = g4 * 4 + i;
+        kr[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(kb + (dc >> 3) * 128 +
+                                                            (e0 ^ ((dc & 7) << 4))));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc = mfma32(kr[i], qb[g4 * 4 + i], sc);
+      __builtin_amdgcn_sched_barrier(0);
     }
 
     float x[16];
@@ -193,13 +203,21 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
       pb1[e] = pack_bf16x2(p[8 + 2 * e], p[8 + 2 * e + 1]);
     }
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint16_t* vrow = vb + (dt * 32 + col) * kSub;
-      const bf16x8 v0 = as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + ((half ^ vsw) << 3)));
-      const bf16x8 v1 =
-          as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + (((2 + half) ^ vsw) << 3)));
-      o[dt] = mfma32(v0, as_bf16x8(pb0), o[dt]);
-      o[dt] = mfma32(v1, as_bf16x8(pb1), o[dt]);
+    for (int d2 = 0; d2 < 4; ++d2) {
+      bf16x8 vr[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint16_t* vrow = vb + ((2 * d2 + i) * 32 + col) * kSub;
+        vr[2 * i] = as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + ((half ^ vsw) << 3)));
+        vr[2 * i + 1] =
+            as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + (((2 + half) ^ vsw) << 3)));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        o[2 * d2 + i] = mfma32(vr[2 * i], as_bf16x8(pb0), o[2 * d2 + i]);
+        o[2 * d2 + i] = mfma32(vr[2 * i + 1], as_bf16x8(pb1), o[2 * d2 + i]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 

@@ -3,6 +3,7 @@ reduction that ``bench.py`` reports as ``roofline.traffic``.
 
 Workloads (run as the program after ``rocprofv3 ... --``):
   python -m exp3_amd.profiling attention [--seq 32640] [--method mean_native] [--repeats 2]
+                                         [--q-heads 28 --kv-heads 4 --head-dim 128] [--dense-impl sdpa]
       one prefill attention layer (pool, route, attention) per repeat, as bench.py runs it
   python -m exp3_amd.profiling copy [--gib 1]
       a plain device copy of known size (torch copy_), the calibration for the
@@ -82,8 +83,10 @@ def run_attention(args) -> None:
     import torch
     from exp3_amd import _lib, attention, synthetic
     _lib.load()
-    q, k, v, _ = synthetic.make_inputs(args.seq, seed=args.seed, device="cuda")
-    backend = attention.AttentionBackend(alpha=args.alpha, register=False)
+    q, k, v, _ = synthetic.make_inputs(args.seq, seed=args.seed, q_heads=args.q_heads,
+                                       kv_heads=args.kv_heads, head_dim=args.head_dim, device="cuda")
+    backend = attention.AttentionBackend(alpha=args.alpha, register=False,
+                                         dense_impl=args.dense_impl)
     backend.configure(args.method, args.alpha)
 
     class Layer:
@@ -91,7 +94,7 @@ def run_attention(args) -> None:
 
     for _ in range(args.repeats):
         backend.forward(Layer(), q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), None,
-                        128 ** -0.5)
+                        args.head_dim ** -0.5)
     torch.cuda.synchronize()
     print(f"attention {args.method} S={args.seq} x{args.repeats} done", flush=True)
 
@@ -116,6 +119,10 @@ def main(argv=None) -> int:
     a.add_argument("--alpha", type=float, default=0.08)
     a.add_argument("--seed", type=int, default=17)
     a.add_argument("--repeats", type=int, default=2)
+    a.add_argument("--q-heads", type=int, default=28)
+    a.add_argument("--kv-heads", type=int, default=4)
+    a.add_argument("--head-dim", type=int, default=128)
+    a.add_argument("--dense-impl", default="sdpa", choices=("sdpa", "hip"))
     c = sub.add_parser("copy")
     c.add_argument("--gib", type=float, default=1.0)
     c.add_argument("--repeats", type=int, default=3)
