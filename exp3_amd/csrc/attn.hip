@@ -462,69 +462,108 @@ __device__ __forceinline__ void full_block(const OperandTables& tb, WaveState& w
 // `ids`) of one query tile into kb / vb (K hi rows i, lo rows 64 + i; value slots
 // 0..63), with per-key biases ln(n_j) log2 e. Threads of one item (128 lanes
 // stride `stride`) cooperate.
+// Tail tile entry i, 8-dim chunk c: the key as bf16 hi + lo rows (i and 64 + i,
+// 16-byte chunks at the swizzled position) and the value in slot value_slot_of_key(i)
+// of each of the chunk's eight dim rows.
+__device__ __forceinline__ void write_tail_entry(uint16_t* kb, uint16_t* vb, int i, int c,
+                                                 const float (&mk)[8], const float (&mv)[8]) {
+  u32x4 hi, lo;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const uint32_t h2 = pack_bf16x2(mk[2 * x], mk[2 * x + 1]);
+    hi[x] = h2;
+    lo[x] = pack_bf16x2(mk[2 * x] - bf16_lo(h2), mk[2 * x + 1] - bf16_hi(h2));
+  }
+  *reinterpret_cast<u32x4*>(kb + swz(i, c)) = hi;
+  *reinterpret_cast<u32x4*>(kb + swz(kTailTile + i, c)) = lo;
+  const int slot = value_slot_of_key(i);
+#pragma unroll
+  for (int x = 0; x < 8; ++x) {
+    const int d = c * 8 + x;
+    vb[swz(d, slot >> 3) + (slot & 7)] = to_bf16_bits(mv[x]);
+  }
+}
+
+__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+  const f32x4 a0 = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 a1 = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { x[e] = a0[e]; x[4 + e] = a1[e]; }
+}
+
+// Block-mean tail tile: entries t0 .. t0 + 63 of `ids` (unselected blocks), key =
+// fp32 mean K split into bf16 hi + lo, value = bf16 mean V, logit bias ln n_j.
+// One work item per (entry, 8-dim chunk).
 __device__ __forceinline__ void stage_tail(const AttnArgs& a, const int16_t* ids, int ntail, int t0,
                                            int64_t desc_base, uint16_t* kb, uint16_t* vb,
                                            float* bias, int tid0, int stride) {
-  for (int e = tid0; e < kTailTile * kHeadDim; e += stride) {
-    const int i = e >> 7, d = e & 127;
+  for (int e = tid0; e < kTailTile * (kHeadDim / 8); e += stride) {
+    const int i = e >> 4, c = e & 15;
     const int j = (t0 + i < ntail) ? (int)ids[t0 + i] : -1;
-    float mk = 0.0f, mv = 0.0f;
+    float mk[8] = {}, mv[8] = {};
     if (j >= 0) {
-      const int64_t off = (desc_base + (int64_t)j * a.kv_heads) * kHeadDim + d;
-      mk = a.mean_k[off];
-      mv = a.mean_v[off];
+      const int64_t off = (desc_base + (int64_t)j * a.kv_heads) * kHeadDim + c * 8;
+      load8(a.mean_k + off, mk);
+      load8(a.mean_v + off, mv);
     }
-    const uint16_t hi = to_bf16_bits(mk);
-    const uint16_t lo = to_bf16_bits(mk - __uint_as_float((uint32_t)hi << 16));
-    kb[swz(i, d >> 3) + (d & 7)] = hi;
-    kb[swz(kTailTile + i, d >> 3) + (d & 7)] = lo;
-    const int slot = value_slot_of_key(i);
-    vb[swz(d, slot >> 3) + (slot & 7)] = to_bf16_bits(mv);
-    if (d == 0) bias[i] = j >= 0 ? logf((float)a.bcounts[j]) * kLog2e : -INFINITY;
+    write_tail_entry(kb, vb, i, c, mk, mv);
+    if (c == 0) bias[i] = j >= 0 ? logf((float)a.bcounts[j]) * kLog2e : -INFINITY;
   }
 }
 
 // Rescue tail tile (kernels.py:233-309): entries per block epb = 1 (the block's
 // rescue token: its key row, its value, logit bias 0) or 2 (also the mean of the
 // other 127 tokens: (mean * 128 - token) / 127 for key and value, bias ln 127
-// log2 e). Blocks t0 .. t0 + kTailTile / epb - 1 of `ids`; K rows as in
-// stage_tail (hi row i, lo row 64 + i), values in slots 0..63. The token's key and
-// value come from the pool pass's key / value tiles of block j.
+// log2 e). Blocks t0 .. t0 + kTailTile / epb - 1 of `ids`; layout as stage_tail.
+// The token's key chunk is one 16-byte read of the pool pass's key tile; its value
+// is a column of the transposed value tile (eight 2-byte reads per chunk).
 __device__ __forceinline__ void stage_rescue(const AttnArgs& a, const int16_t* ids, int ntail,
                                              int t0, int epb, int b, int g, int h, int t,
                                              uint16_t* kb, uint16_t* vb, float* bias, int tid0,
                                              int stride) {
   const int64_t tile_elems = (int64_t)kBlock * kHeadDim;
-  for (int e = tid0; e < kTailTile * kHeadDim; e += stride) {
-    const int i = e >> 7, d = e & 127;
+  for (int e = tid0; e < kTailTile * (kHeadDim / 8); e += stride) {
+    const int i = e >> 4, c = e & 15;
     const int blk = t0 + i / epb, kind = i % epb;
     const int j = blk < ntail ? (int)ids[blk] : -1;
-    float mk = 0.0f, mv = 0.0f, bi = -INFINITY;
+    float mk[8] = {}, mv[8] = {};
+    float bi = -INFINITY;
     if (j >= 0) {
       const int tok = a.choice[(((int64_t)b * a.blocks + t) * a.blocks + j) * a.q_heads + h];
       const int64_t tile = (((int64_t)b * a.kv_heads + g) * a.blocks + j) * tile_elems;
-      const float kval =
-          __uint_as_float((uint32_t)a.kt[tile + tok * kHeadDim + swz_off(tok, d)] << 16);
+      const u32x4 kraw =
+          *reinterpret_cast<const u32x4*>(a.kt + tile + tok * kHeadDim + ((c ^ (tok & 15)) << 3));
       const int slot = value_slot_of_key(tok);
-      const float vval = __uint_as_float((uint32_t)a.vt[tile + d * kBlock + swz_off(d, slot)] << 16);
+      float kval[8], vval[8];
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        kval[2 * x] = bf16_lo(kraw[x]);
+        kval[2 * x + 1] = bf16_hi(kraw[x]);
+      }
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        const int d = c * 8 + x;
+        vval[x] = __uint_as_float((uint32_t)a.vt[tile + d * kBlock + swz_off(d, slot)] << 16);
+      }
       if (kind == 0) {
-        mk = kval;
-        mv = vval;
+#pragma unroll
+        for (int x = 0; x < 8; ++x) { mk[x] = kval[x]; mv[x] = vval[x]; }
         bi = 0.0f;
       } else {
-        const int64_t off = (((int64_t)b * a.blocks + j) * a.kv_heads + g) * kHeadDim + d;
-        mk = (a.mean_k[off] * (float)kBlock - kval) / (float)(kBlock - 1);
-        mv = (a.mean_v[off] * (float)kBlock - vval) / (float)(kBlock - 1);
+        const int64_t off = (((int64_t)b * a.blocks + j) * a.kv_heads + g) * kHeadDim + c * 8;
+        float mean_k[8], mean_v[8];
+        load8(a.mean_k + off, mean_k);
+        load8(a.mean_v + off, mean_v);
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+          mk[x] = (mean_k[x] * (float)kBlock - kval[x]) / (float)(kBlock - 1);
+          mv[x] = (mean_v[x] * (float)kBlock - vval[x]) / (float)(kBlock - 1);
+        }
         bi = logf((float)(kBlock - 1)) * kLog2e;
       }
     }
-    const uint16_t hi = to_bf16_bits(mk);
-    const uint16_t lo = to_bf16_bits(mk - __uint_as_float((uint32_t)hi << 16));
-    kb[swz(i, d >> 3) + (d & 7)] = hi;
-    kb[swz(kTailTile + i, d >> 3) + (d & 7)] = lo;
-    const int vslot = value_slot_of_key(i);
-    vb[swz(d, vslot >> 3) + (vslot & 7)] = to_bf16_bits(mv);
-    if (d == 0) bias[i] = bi;
+    write_tail_entry(kb, vb, i, c, mk, mv);
+    if (c == 0) bias[i] = bi;
   }
 }
 

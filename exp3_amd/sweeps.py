@@ -8,6 +8,11 @@
   python -m exp3_amd.sweeps long [--seq 131072] [--needles 256]
       long context: cgf_mean and dispersion_mean at alpha 0.04 (plus mean_native
       at 0.04 for reference), same columns
+  python -m exp3_amd.sweeps sparse [--seq 32640] [--qk-scale 4]
+      sparse selections (not a BASELINE config): the seeded inputs with Q and K
+      multiplied by --qk-scale (bf16) sharpen the block scores, and alpha in
+      {0.08, 0.3, 0.5, 0.7} gives densities well below 1, exercising the block-mean
+      and rescue tails; mean_native, fp_v1, cgf_mean, fp_v1_rescue_v2 and dense
   python -m exp3_amd.sweeps d256 [--seq 32640]
       head_dim 256 with 16 query / 4 KV heads (Qwen3.5 full-attention layer shape,
       check_qwen35_math.py): dense (torch SDPA and the HIP kernel) and fp_v1 at
@@ -93,6 +98,22 @@ def run_layer_sweep(seq, needles, seed, cases, label):
     for method, alpha in cases:
         row = _layer_case(torch, attention, kernels, q, k, v, method, alpha)
         row.update({"sweep": label, "needles": needles, "seed": seed})
+        print(json.dumps(row), flush=True)
+
+
+def run_sparse(seq, seed, qk_scale):
+    import torch
+    from exp3_amd import _lib, attention, kernels, synthetic
+    _lib.load()
+    q, k, v, _ = synthetic.make_inputs(seq, seed=seed, device="cuda")
+    q = (q.float() * qk_scale).to(torch.bfloat16)
+    k = (k.float() * qk_scale).to(torch.bfloat16)
+    cases = [(m, a) for a in (0.08, 0.3, 0.5, 0.7)
+             for m in ("mean_native", "fp_v1", "cgf_mean", "fp_v1_rescue_v2")]
+    cases.append(("dense", 0.08))
+    for method, alpha in cases:
+        row = _layer_case(torch, attention, kernels, q, k, v, method, alpha)
+        row.update({"sweep": "sparse", "qk_scale": qk_scale, "seed": seed})
         print(json.dumps(row), flush=True)
 
 
@@ -189,6 +210,10 @@ def main(argv=None) -> int:
     lo.add_argument("--seq", type=int, default=131072)
     lo.add_argument("--needles", type=int, default=256)
     lo.add_argument("--seed", type=int, default=17)
+    sp = sub.add_parser("sparse")
+    sp.add_argument("--seq", type=int, default=32640)
+    sp.add_argument("--seed", type=int, default=17)
+    sp.add_argument("--qk-scale", type=float, default=4.0)
     d2 = sub.add_parser("d256")
     d2.add_argument("--seq", type=int, default=32640)
     d2.add_argument("--seed", type=int, default=17)
@@ -205,6 +230,8 @@ def main(argv=None) -> int:
         cases = [(m, a) for a in (0.04, 0.08, 0.16) for m in MEAN_FOUR]
         cases += [("fp_v1", 0.08), ("dense", 0.08)]
         run_layer_sweep(args.seq, args.needles, args.seed, cases, "needles")
+    elif args.cmd == "sparse":
+        run_sparse(args.seq, args.seed, args.qk_scale)
     elif args.cmd == "d256":
         run_d256(args.seq, args.seed)
     elif args.cmd == "long":
