@@ -125,3 +125,31 @@ def test_tails_batch2(gpu, method):
     if differ == 0:
         # peaked attention: outputs beyond unit scale, one bf16 step relative on top
         assert_output_close(to_np(out), expected["output"], what=method, rel=2.0 ** -7)
+
+
+@pytest.mark.parametrize("length", (1, 100, 128, 129, 256))
+@pytest.mark.parametrize("method", attention.METHODS)
+def test_short_and_boundary_lengths(gpu, method, length):
+    """One token, a partial single block, exact block multiples and one token past
+    a block: every method against the oracle layer."""
+    q, k, v, _ = synthetic.make_inputs(length, seed=73)
+    backend = attention.AttentionBackend(alpha=0.08, register=False)
+    backend.configure(method, 0.08)
+    out, _ = backend.forward(_Layer(), q.cuda().transpose(1, 2), k.cuda().transpose(1, 2),
+                             v.cuda().transpose(1, 2), None, SCALE)
+    expected = ref.attention_layer(to_np(q), to_np(k), to_np(v), SCALE, method, 0.08)
+    assert out.shape == (1, length, 28, 128)
+    assert_output_close(to_np(out), expected["output"], what=f"{method} S={length}")
+
+
+@pytest.mark.parametrize("length", (1, 100))
+def test_short_lengths_d256(gpu, length):
+    q, k, v, _ = synthetic.make_inputs(length, seed=79, q_heads=16, kv_heads=4, head_dim=256)
+    scale = 256 ** -0.5
+    for method, impl in (("fp_v1", "sdpa"), ("dense", "hip")):
+        backend = attention.AttentionBackend(alpha=0.08, register=False, dense_impl=impl)
+        backend.configure(method, 0.08)
+        out, _ = backend.forward(_Layer(), q.cuda().transpose(1, 2), k.cuda().transpose(1, 2),
+                                 v.cuda().transpose(1, 2), None, scale)
+        expected = ref.attention_layer(to_np(q), to_np(k), to_np(v), scale, method, 0.08)
+        assert_output_close(to_np(out), expected["output"], what=f"d256 {method} S={length}")
