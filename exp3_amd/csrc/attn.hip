@@ -458,10 +458,6 @@ __device__ __forceinline__ void full_block(const OperandTables& tb, WaveState& w
   }
 }
 
-// Mean-correction tail tile: stage up to kTailTile unselected blocks (ids from
-// `ids`) of one query tile into kb / vb (K hi rows i, lo rows 64 + i; value slots
-// 0..63), with per-key biases ln(n_j) log2 e. Threads of one item (128 lanes
-// stride `stride`) cooperate.
 // Tail tile entry i, 8-dim chunk c: the key as bf16 hi + lo rows (i and 64 + i,
 // 16-byte chunks at the swizzled position) and the value in slot value_slot_of_key(i)
 // of each of the chunk's eight dim rows.
