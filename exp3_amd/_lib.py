@@ -18,7 +18,7 @@ SPX_OK = 0
 SPX_EINVAL = -1
 SPX_EUNSUPPORTED = -2
 SPX_ELAUNCH = -3
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 SELECTOR_IDS = {"mean_balanced": 0, "cgf_mean": 1, "dispersion_mean": 2}
 
@@ -51,10 +51,10 @@ _PROTOTYPES = {
     "spx_selection_accounting": [_P, _I, _I, _I, _I, _I, _I, _P, _P],
     "spx_tile_mean_query": [_P, _S, _I, _I, _I, _I, _I, _P, _P],
     "spx_rescue_choice": [_P, _P, _I, _I, _I, _I, _I, _I, _P, _P],
-    "spx_rescue_tail": [_P, _S, _P, _P, _P, _S, _P, _S, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
-                        _F, _P, _S, _P, _S, _P],
-    "spx_sparse_attention_rescue": [_P, _S, _P, _P, _P, _S, _P, _S, _P, _P, _P, _I, _I, _I, _I,
-                                    _I, _I, _I, _F, _P, _S, _P, _S, _P],
+    "spx_rescue_tail": [_P, _S, _P, _P, _P, _S, _P, _S, _P, _P, _S, _P, _P, _I, _I, _I, _I, _I,
+                        _I, _I, _F, _P, _S, _P, _S, _P],
+    "spx_sparse_attention_rescue": [_P, _S, _P, _P, _P, _S, _P, _S, _P, _P, _S, _P, _P, _I, _I,
+                                    _I, _I, _I, _I, _I, _F, _P, _S, _P, _S, _P],
 }
 
 # helpers with other return types

@@ -10,12 +10,15 @@ runs entirely in gfx950 HIP kernels:
   selector    spx_v1_route             V1 score + normalise + threshold selection
               spx_selector_scores      (mean_balanced / cgf_mean / dispersion_mean)
   indices     spx_protected_selection  (new selectors; V1 selection is fused above)
+  mean        spx_tile_mean_query +    rescue-token choice (rescue methods only)
+              spx_rescue_choice
   exact       spx_exact_attention      block-sparse flash attention
               spx_sparse_attention_mean  same, with the mean tail and the
                                          logaddexp merge fused in (mean methods)
+              spx_sparse_attention_rescue  same, with the rescue tail fused in
 
-so the reference's separate "mean" and "merge" stages take no time here and are
-reported as 0 ms. Dense prefill and every decode step use
+so the reference's separate "merge" stage (and, for the mean methods, its "mean"
+stage) takes no time here and is reported as 0 ms. Dense prefill and every decode step use
 ``F.scaled_dot_product_attention`` exactly as the reference does
 (attention.py:179-189); ``dense_impl="hip"`` routes dense prefill through the
 HIP kernel with implicit all-causal block lists instead.
@@ -207,7 +210,7 @@ class AttentionBackend:
                    rescue=None):
         """One attention-kernel launch: exact blocks, plus the block-mean tail
         (``descriptors``) or the rescue tail (``rescue`` = (choice, remainder,
-        descriptors-or-None)) in the same online softmax."""
+        descriptors-or-None, v)) in the same online softmax."""
         device = q.device
         batch, sequence, q_heads, head_dim = q.shape
         output = torch.empty(batch, sequence, q_heads, head_dim, dtype=q.dtype, device=device)
@@ -223,8 +226,9 @@ class AttentionBackend:
             events = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             events[0].record()
         if rescue is not None:
-            choice, remainder, rdesc = rescue
+            choice, remainder, rdesc, values = rescue
             _lib.call("spx_sparse_attention_rescue", *common_head, _lib.ptr(choice),
+                      _lib.ptr(values), _lib.strides(values),
                       _lib.ptr(rdesc.mean_k if rdesc else None),
                       _lib.ptr(rdesc.mean_v if rdesc else None), int(remainder), *common_tail)
         elif descriptors is None:
@@ -316,7 +320,7 @@ class AttentionBackend:
                 choice = self._stage(
                     record, "mean",
                     lambda: kernels.rescue_choice(q, tiles[0], self.block_size))
-                rescue = (choice, self.method == "fp_v1_rescue_v2", descriptors)
+                rescue = (choice, self.method == "fp_v1_rescue_v2", descriptors, v)
             output, _ = self._stage(
                 record, "exact",
                 lambda: self._attention(q, k, tiles, indices, counts, scale, mean_desc, rescue))

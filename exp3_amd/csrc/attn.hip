@@ -60,6 +60,8 @@ struct AttnArgs {
   const float* mean_v;
   const int32_t* bcounts;  // [NB]
   const uint8_t* choice;   // rescue token per (b, t, j, h): [B, NB, NB, Hq]
+  const uint16_t* v;       // V [B, S, Hkv, D] (strided): rescue tokens' value rows
+  int64_t vs_b, vs_s, vs_h;
   int tail_kind;           // 0 block means, 1 rescue token, 2 rescue token + remainder mean
   void* out;
   int64_t os_b, os_s, os_h;
@@ -511,8 +513,9 @@ __device__ __forceinline__ void stage_tail(const AttnArgs& a, const int16_t* ids
 // rescue token: its key row, its value, logit bias 0) or 2 (also the mean of the
 // other 127 tokens: (mean * 128 - token) / 127 for key and value, bias ln 127
 // log2 e). Blocks t0 .. t0 + kTailTile / epb - 1 of `ids`; layout as stage_tail.
-// The token's key chunk is one 16-byte read of the pool pass's key tile; its value
-// is a column of the transposed value tile (eight 2-byte reads per chunk).
+// The token's key chunk is one 16-byte read of the pool pass's key tile, its value
+// chunk one 16-byte read of its row of V (history blocks j < t are full, so the
+// token is inside the sequence).
 __device__ __forceinline__ void stage_rescue(const AttnArgs& a, const int16_t* ids, int ntail,
                                              int t0, int epb, int b, int g, int h, int t,
                                              uint16_t* kb, uint16_t* vb, float* bias, int tid0,
@@ -529,17 +532,15 @@ __device__ __forceinline__ void stage_rescue(const AttnArgs& a, const int16_t* i
       const int64_t tile = (((int64_t)b * a.kv_heads + g) * a.blocks + j) * tile_elems;
       const u32x4 kraw =
           *reinterpret_cast<const u32x4*>(a.kt + tile + tok * kHeadDim + ((c ^ (tok & 15)) << 3));
-      const int slot = value_slot_of_key(tok);
+      const u32x4 vraw = *reinterpret_cast<const u32x4*>(
+          a.v + b * a.vs_b + ((int64_t)j * kBlock + tok) * a.vs_s + g * a.vs_h + c * 8);
       float kval[8], vval[8];
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         kval[2 * x] = bf16_lo(kraw[x]);
         kval[2 * x + 1] = bf16_hi(kraw[x]);
-      }
-#pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        const int d = c * 8 + x;
-        vval[x] = __uint_as_float((uint32_t)a.vt[tile + d * kBlock + swz_off(d, slot)] << 16);
+        vval[2 * x] = bf16_lo(vraw[x]);
+        vval[2 * x + 1] = bf16_hi(vraw[x]);
       }
       if (kind == 0) {
 #pragma unroll
@@ -888,6 +889,8 @@ struct AttnRequest {
   bool exact, tail, out_f32;
   int tail_kind;             // 0 block means, 1 rescue token, 2 rescue token + remainder
   const uint8_t* choice;     // rescue tokens (tail_kind > 0)
+  const void* v;             // V rows of the rescue tokens (tail_kind > 0)
+  const int64_t* v_strides;
 };
 
 int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_strides,
@@ -929,6 +932,8 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
                 SPX_EINVAL, "rescue tail needs 16-byte aligned key_tiles and value_tiles");
     SPX_REQUIRE(req.tail_kind == 1 || (mean_k && mean_v), SPX_EINVAL,
                 "rescue remainder needs mean_k and mean_v");
+    int ev = check_bsdh("v", req.v, req.v_strides, true);
+    if (ev) return ev;
   }
   if (indices) {
     SPX_REQUIRE(index_strides && counts && count_strides, SPX_EINVAL,
@@ -956,6 +961,10 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
   }
   a.mean_k = mean_k; a.mean_v = mean_v; a.bcounts = block_counts;
   a.choice = req.choice; a.tail_kind = req.tail ? req.tail_kind : 0;
+  if (req.tail && req.tail_kind > 0) {
+    a.v = static_cast<const uint16_t*>(req.v);
+    a.vs_b = req.v_strides[0]; a.vs_s = req.v_strides[1]; a.vs_h = req.v_strides[2];
+  }
   a.out = out;
   a.os_b = out_strides[0]; a.os_s = out_strides[1]; a.os_h = out_strides[2];
   a.lse = lse;
@@ -1063,11 +1072,12 @@ extern "C" int spx_merge_exact_mean(const void* exact_out, const int64_t* exact_
 extern "C" int spx_sparse_attention_rescue(
     const void* q, const int64_t* q_strides, const void* key_tiles, const void* value_tiles,
     const int64_t* indices, const int64_t* index_strides, const int32_t* counts,
-    const int64_t* count_strides, const uint8_t* choice, const float* mean_k, const float* mean_v,
-    int remainder, int batch, int seq, int q_heads, int kv_heads, int head_dim, int block_size,
-    float scale, void* out, const int64_t* out_strides, float* lse, const int64_t* lse_strides,
-    void* stream) {
-  return launch_attention({true, true, false, remainder ? 2 : 1, choice}, q, q_strides, key_tiles,
+    const int64_t* count_strides, const uint8_t* choice, const void* v, const int64_t* v_strides,
+    const float* mean_k, const float* mean_v, int remainder, int batch, int seq, int q_heads,
+    int kv_heads, int head_dim, int block_size, float scale, void* out, const int64_t* out_strides,
+    float* lse, const int64_t* lse_strides, void* stream) {
+  return launch_attention({true, true, false, remainder ? 2 : 1, choice, v, v_strides}, q, q_strides,
+                          key_tiles,
                           value_tiles, indices, index_strides, counts, count_strides, mean_k,
                           mean_v, nullptr, batch, seq, q_heads, kv_heads, head_dim, block_size,
                           scale, out, out_strides, lse, lse_strides, stream);
@@ -1077,12 +1087,14 @@ extern "C" int spx_rescue_tail(const void* q, const int64_t* q_strides, const vo
                                const void* value_tiles, const int64_t* indices,
                                const int64_t* index_strides, const int32_t* counts,
                                const int64_t* count_strides, const uint8_t* choice,
-                               const float* mean_k, const float* mean_v, int remainder, int batch,
-                               int seq, int q_heads, int kv_heads, int head_dim, int block_size,
-                               float scale, float* out, const int64_t* out_strides, float* lse,
-                               const int64_t* lse_strides, void* stream) {
+                               const void* v, const int64_t* v_strides, const float* mean_k,
+                               const float* mean_v, int remainder, int batch, int seq, int q_heads,
+                               int kv_heads, int head_dim, int block_size, float scale, float* out,
+                               const int64_t* out_strides, float* lse, const int64_t* lse_strides,
+                               void* stream) {
   SPX_REQUIRE(indices != nullptr, SPX_EINVAL, "rescue_tail: indices must be given");
-  return launch_attention({false, true, true, remainder ? 2 : 1, choice}, q, q_strides, key_tiles,
+  return launch_attention({false, true, true, remainder ? 2 : 1, choice, v, v_strides}, q, q_strides,
+                          key_tiles,
                           value_tiles, indices, index_strides, counts, count_strides, mean_k,
                           mean_v, nullptr, batch, seq, q_heads, kv_heads, head_dim, block_size,
                           scale, out, out_strides, lse, lse_strides, stream);

@@ -235,14 +235,16 @@ def rescue_tail(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, selected: tor
         raise ValueError(f"selected shape {tuple(selected.shape)}, expected "
                          f"{(batch, blocks, blocks, q_heads)}")
     key_tiles, value_tiles, mean_k, mean_v = _pool_tiles_and_means(k, v, block_size)
+    values = _lib.kernel_view(v)
     choice = rescue_choice(q, key_tiles, block_size)
     indices, counts = indices_from_mask(selected)
     output = torch.empty(batch, sequence, q_heads, head_dim, dtype=torch.float32, device=device)
     lse = torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
     _lib.call("spx_rescue_tail", _lib.ptr(q), _lib.strides(q), _lib.ptr(key_tiles),
               _lib.ptr(value_tiles), _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
-              _lib.strides(counts), _lib.ptr(choice), _lib.ptr(mean_k), _lib.ptr(mean_v),
-              int(bool(remainder)), batch, sequence, q_heads, k.shape[2], head_dim, block_size,
+              _lib.strides(counts), _lib.ptr(choice), _lib.ptr(values), _lib.strides(values),
+              _lib.ptr(mean_k), _lib.ptr(mean_v), int(bool(remainder)), batch, sequence, q_heads,
+              k.shape[2], head_dim, block_size,
               float(scale), _lib.ptr(output), _lib.strides(output), _lib.ptr(lse),
               _lib.strides(lse), _lib.stream(device))
     return output, lse

@@ -40,7 +40,7 @@ extern "C" {
 #define SPX_EUNSUPPORTED (-2) /* valid in the reference, not built here       */
 #define SPX_ELAUNCH (-3)      /* HIP launch / runtime failure                 */
 
-#define SPX_ABI_VERSION 4
+#define SPX_ABI_VERSION 5
 
 /* Selector ids for spx_selector_scores (kernels.py:62). */
 #define SPX_SELECTOR_MEAN_BALANCED 0
@@ -242,23 +242,26 @@ int spx_rescue_choice(const float* qmean, const void* key_tiles, int batch, int 
  * and value, logit scale q.k) and, with remainder != 0, a second entry with the mean
  * K / V of the block's other 127 tokens (logit + ln 127). Selection as index lists;
  * mean_k / mean_v (fp32 [B, NB, Hkv, D], from spx_block_descriptors) are read only
- * with remainder. Replaces kernels.py:233-309 (rescue_tail). */
+ * with remainder. v: the layer's V [B, S, Hkv, D] bf16 (strided, 16-byte aligned
+ * rows): the tokens' value rows. Replaces kernels.py:233-309 (rescue_tail). */
 int spx_rescue_tail(const void* q, const int64_t* q_strides, const void* key_tiles,
                     const void* value_tiles, const int64_t* indices, const int64_t* index_strides,
                     const int32_t* counts, const int64_t* count_strides, const uint8_t* choice,
+                    const void* v, const int64_t* v_strides,
                     const float* mean_k, const float* mean_v, int remainder, int batch, int seq,
                     int q_heads, int kv_heads, int head_dim, int block_size, float scale,
                     float* out, const int64_t* out_strides, float* lse,
                     const int64_t* lse_strides, void* stream);
 
 /* Exact attention with the rescue path fused into the same online softmax (equal
- * to the logaddexp merge of the two). Replaces the exact + rescue + merge stages of
+ * to the logaddexp merge of the two); arguments as spx_rescue_tail. Replaces the exact + rescue + merge stages of
  * attention.py:306-331 (fp_v1_rescue / fp_v1_rescue_v2): upstream exact_attention,
  * kernels.py:233-309 (rescue_tail) and kernels.py:312-325 (merge_exact_mean). */
 int spx_sparse_attention_rescue(const void* q, const int64_t* q_strides, const void* key_tiles,
                                 const void* value_tiles, const int64_t* indices,
                                 const int64_t* index_strides, const int32_t* counts,
                                 const int64_t* count_strides, const uint8_t* choice,
+                                const void* v, const int64_t* v_strides,
                                 const float* mean_k, const float* mean_v, int remainder,
                                 int batch, int seq, int q_heads, int kv_heads, int head_dim,
                                 int block_size, float scale, void* out,
