@@ -27,7 +27,11 @@
       use_cache=True, logits_to_keep=1), argmax, sync; each method warmed up
       first (evaluate.py:634-644), repeats with rotated method order
       (evaluate.py:646-663), median reported (report.py:33-42); then 128 greedy
-      dense decode tokens (not timed) to exercise the decode path.
+      dense decode tokens (not timed) to exercise the decode path. With
+      --split-last-token, each method also runs evaluate.py:357-380's RULER flow:
+      prefill of the first S - 1 ids through the backend, then the last id as one
+      cached decode step; its first greedy id is printed beside the full
+      prefill's.
 
 Every run prints one JSON object per measured case.
 """
@@ -141,7 +145,7 @@ def qwen2_7b_config(layers):
                        attn_implementation="sdpa", torch_dtype="bfloat16")
 
 
-def run_model(seq, layers, repeats, seed, methods, alpha, decode_tokens):
+def run_model(seq, layers, repeats, seed, methods, alpha, decode_tokens, split_last=False):
     import torch
     from transformers import Qwen2ForCausalLM
     from exp3_amd import _lib, attention
@@ -185,6 +189,19 @@ def run_model(seq, layers, repeats, seed, methods, alpha, decode_tokens):
                           "prefill_ms_all": [round(x, 1) for x in times[m]],
                           "speedup_vs_dense": round(dense_ms / med, 3) if dense_ms else None}),
               flush=True)
+    if split_last:   # evaluate.py:357-380, split_last_prompt_token=True (not timed)
+        for m in methods:
+            _, _, full_token = prefill(m)
+            with torch.no_grad():
+                pre = model.model(input_ids=ids[:, :-1], use_cache=True)
+                step = model(input_ids=ids[:, -1:], past_key_values=pre.past_key_values,
+                             use_cache=True, logits_to_keep=1,
+                             cache_position=torch.tensor([seq - 1], device="cuda"))
+                split_token = step.logits[:, -1].argmax(-1)
+            del pre, step
+            print(json.dumps({"sweep": "model-split-last-token", "method": m, "seq": seq,
+                              "full_prefill_id": int(full_token.item()),
+                              "split_id": int(split_token.item())}), flush=True)
     # greedy dense decode (not timed): exercises the backend's decode branch
     _, out, token = prefill("dense")
     cache = out.past_key_values
@@ -224,6 +241,7 @@ def main(argv=None) -> int:
     mo.add_argument("--seed", type=int, default=17)
     mo.add_argument("--alpha", type=float, default=0.08)
     mo.add_argument("--decode-tokens", type=int, default=128)
+    mo.add_argument("--split-last-token", action="store_true")
     mo.add_argument("--methods", default="dense,fp_v1,mean_native,mean_balanced,cgf_mean,dispersion_mean")
     args = p.parse_args(argv)
     if args.cmd == "needles":
@@ -239,7 +257,7 @@ def main(argv=None) -> int:
         run_layer_sweep(args.seq, args.needles, args.seed, cases, "long")
     else:
         run_model(args.seq, args.layers, args.repeats, args.seed, args.methods.split(","),
-                  args.alpha, args.decode_tokens)
+                  args.alpha, args.decode_tokens, args.split_last_token)
     return 0
 
 
