@@ -99,6 +99,8 @@ struct WaveState {
   f32x16 o[4];    // O^T accumulators, dim block db
   float m;        // running max (base-2, scaled), lazily moved
   float l;        // running sum over this lane half's keys
+  float neg_m;    // full blocks: -m once set (0 before)
+  float thr;      // full blocks: lazy-move threshold on shifted scores (-inf before m is set)
 };
 
 // Copy one 32 KB tile, already in LDS order in global memory, into LDS with
@@ -288,15 +290,16 @@ __device__ __forceinline__ void exact_block(const uint16_t* kb, const uint16_t* 
 
 // ---------------------------------------------------------------- full blocks
 // A full (unmasked) block, software-pipelined over its four 32-key sub-blocks so
-// that one wave overlaps its own exponentials with its matrix work:
+// that each group of eight MFMAs carries about half of one sub-block's softmax:
 //
-//   step 0: scores S0
-//   step k: P V of sub-block k-2 | max of S(k-1) | rescale | scores S(k) with the
-//           exponentials of S(k-1) in between            (k = 1..4, as they exist)
-//   step 5: P V of sub-block 3
+//   step 0: P V of the previous full block's sub-block 3 | scores S0
+//   step k: P V of sub-block k-2 (k >= 2) with the shift and max of S(k-1) |
+//           lazy rescale | scores S(k) (k <= 3) with the exponentials of S(k-1)
+//                                                                   (k = 1..4)
 //
-// The running max moves lazily per sub-block (only when a column's scaled max
-// exceeds it by more than 2^8); the rescale of O comes after the P V products that
+// Sub-block 3's P V product stays pending in registers across the next block's
+// barrier. The running max moves lazily per sub-block (only when a column's
+// shifted max exceeds 2^8); the rescale of O comes after the P V products that
 // used the old max were issued and before any that use the new one.
 //
 // LDS operand addresses: entry c of a table is the byte address of 16-byte chunk
@@ -365,22 +368,28 @@ __device__ __forceinline__ void sub_pv(const bf16x8 (&r)[8], const bf16x8 (&p)[2
     for (int db = 0; db < 4; ++db) ws.o[db] = mfma32(r[h * 4 + db], p[h], ws.o[db]);
 }
 
-// column max of one sub-block (both lane halves hold keys of the same column)
-__device__ __forceinline__ float sub_max(const f32x16& sv) {
+// Shift one sub-block's scores in place to x = s * scale + ws.neg_m (this lane's
+// 16 keys of its column) and check them against the running max. The max runs
+// over the shifted values: results of arithmetic, which the compiler's max takes
+// without quieting them first. The running max moves lazily: only when a
+// column's x exceeds ws.thr (2^8 once set); then (rarely) O and l are rescaled
+// and x shifted by the same amount. Before the first move neg_m is 0 and thr
+// -inf, so the first sub-block sets the max from its own scores.
+__device__ __forceinline__ void shift_and_check(f32x16& sv, WaveState& ws, float scale) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sv[r] = fmaf(sv[r], scale, ws.neg_m);
   float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
 #pragma unroll
   for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sv[r]), sv[r + 1]);
   mx = fmaxf(mx, sv[15]);
   const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false,
                                                    false);
-  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-}
-
-__device__ __forceinline__ void lazy_rescale(WaveState& ws, float mxs) {
-  const bool move = mxs > ws.m + kLazyRescale;
+  mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+  const bool move = mx > ws.thr;
   if (__any(move)) {
-    const float m_new = move ? mxs : ws.m;
-    const float corr = move ? exp2_fast(ws.m - m_new) : 1.0f;
+    const float d = move ? mx : 0.0f;
+    // nothing is accumulated before the first move (thr -inf): O and l stay 0
+    const float corr = ws.thr == -INFINITY ? 0.0f : exp2_fast(-d);
     // in place (tied operands): O keeps its registers across the rarely taken branch
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
@@ -388,7 +397,10 @@ __device__ __forceinline__ void lazy_rescale(WaveState& ws, float mxs) {
       for (int r = 0; r < 16; ++r) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(ws.o[db][r]) : "v"(corr));
     }
     ws.l *= corr;
-    ws.m = m_new;
+    ws.neg_m -= d;
+    if (move) ws.thr = kLazyRescale;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sv[r] -= d;
   }
 }
 
@@ -400,19 +412,17 @@ __device__ __forceinline__ float add_bf16_pair(float acc, uint32_t pair) {
   return acc;
 }
 
-// probabilities of one sub-block as bf16 B operands; the running sum adds the
-// rounded values (the ones the P V product uses)
-__device__ __forceinline__ void sub_exp(const f32x16& sv, WaveState& ws, float scale,
-                                        bf16x8 (&p)[2]) {
-  const float neg_m = -ws.m;
+// probabilities of one sub-block (shifted scores x) as bf16 B operands; the
+// running sum adds the rounded values (the ones the P V product uses)
+__device__ __forceinline__ void sub_exp(const f32x16& xv, WaveState& ws, bf16x8 (&p)[2]) {
   float l = ws.l;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     u32x4 w;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float a = exp2_fast(fmaf(sv[8 * h + 2 * i], scale, neg_m));
-      const float b = exp2_fast(fmaf(sv[8 * h + 2 * i + 1], scale, neg_m));
+      const float a = exp2_fast(xv[8 * h + 2 * i]);
+      const float b = exp2_fast(xv[8 * h + 2 * i + 1]);
       w[i] = pack_bf16x2(a, b);
       l = add_bf16_pair(l, w[i]);
     }
@@ -430,34 +440,39 @@ struct NextCopy {
   bool any;
 };
 
+// One full block in buffer BUF. The previous full block's last P V product
+// (value operands rv, probabilities pend) runs first, beside this block's first
+// key reads; this block's own last product is left in rv / pend. A pending
+// product of zero probabilities and values (the initial state) adds nothing.
 template <int BUF>
-__device__ __forceinline__ void full_block(const OperandTables& tb, WaveState& ws, float scale) {
+__device__ __forceinline__ void full_block(const OperandTables& tb, WaveState& ws, float scale,
+                                           bf16x8 (&rv)[8], bf16x8 (&pend)[2]) {
   f32x16 s[2];
   bf16x8 p[2][2];
-  bf16x8 rv[8], rk[8];
+  bf16x8 rk[8];
   // Each operand group is read one MFMA group ahead: the key reads of step k land
   // during the P V products of step k, the value reads for step k + 1 during the
-  // scores of step k.
+  // scores of step k. The shift and max of S(k-1) run beside the P V products,
+  // its exponentials beside the scores S(k).
   sub_keys<BUF>(tb, 0, rk);
   fence();
+  sub_pv(rv, pend, ws);
   sub_scores(rk, ws, s[0]);
 #pragma unroll
-  for (int k = 1; k <= 5; ++k) {
+  for (int k = 1; k <= 4; ++k) {
     fence();
     if (k <= 3) sub_keys<BUF>(tb, k, rk);
     fence();
-    float mx = 0.0f;
-    if (k <= 4) mx = sub_max(s[(k - 1) & 1]);
     if (k >= 2) sub_pv(rv, p[(k - 2) & 1], ws);
-    if (k <= 4) {
-      lazy_rescale(ws, mx * scale);
-      fence();
-      sub_values<BUF>(tb, k - 1, rv);
-      fence();
-      if (k <= 3) sub_scores(rk, ws, s[k & 1]);
-      sub_exp(s[(k - 1) & 1], ws, scale, p[(k - 1) & 1]);
-    }
+    shift_and_check(s[(k - 1) & 1], ws, scale);
+    fence();
+    sub_values<BUF>(tb, k - 1, rv);
+    fence();
+    if (k <= 3) sub_scores(rk, ws, s[k & 1]);
+    sub_exp(s[(k - 1) & 1], ws, p[(k - 1) & 1]);
   }
+  pend[0] = p[1][0];
+  pend[1] = p[1][1];
 }
 
 // Tail tile entry i, 8-dim chunk c: the key as bf16 hi + lo rows (i and 64 + i,
@@ -618,6 +633,8 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
     }
     ws.m = -INFINITY;
     ws.l = 0.0f;
+    ws.neg_m = 0.0f;
+    ws.thr = -INFINITY;
 #pragma unroll
     for (int db = 0; db < 4; ++db) ws.o[db] = f32x16{};
   }
@@ -694,6 +711,10 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
     };
     const OperandTables tables = operand_tables(kbuf[0], vbuf[0]);
     int u = 0;
+    bf16x8 rv[8], pend[2];  // the pending P V product of the last full block
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rv[i] = bf16x8{};
+    pend[0] = pend[1] = bf16x8{};
     // Full blocks: publish block u, then run it while its successor is copied (by
     // full_block, spread over its steps; here at once if this item skips block u).
     auto run_full = [&](int uu, auto buf) {
@@ -712,12 +733,14 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
         dma_tile(nx.k, nx.kd, tid);
         dma_tile(nx.v, nx.vd, tid);
       }
-      if ((f >> item) & 1) full_block<B>(tables, ws, scale);
+      if ((f >> item) & 1) full_block<B>(tables, ws, scale, rv, pend);
     };
     for (; u < n_full; u += 2) {  // unrolled by two: each block's buffer is a constant
       run_full(u, std::integral_constant<int, 0>{});
       if (u + 1 < n_full) run_full(u + 1, std::integral_constant<int, 1>{});
     }
+    sub_pv(rv, pend, ws);
+    if (ws.thr != -INFINITY) ws.m = -ws.neg_m;  // the max the full blocks settled on
     u = n_full;
     for (; u < nu; ++u) {
       const int cur = u & 1;
