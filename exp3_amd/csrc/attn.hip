@@ -374,19 +374,23 @@ __device__ __forceinline__ void sub_pv(const bf16x8 (&r)[8], const bf16x8 (&p)[2
 // without quieting them first. The running max moves lazily: only when a
 // column's x exceeds ws.thr (2^8 once set); then (rarely) O and l are rescaled
 // and x shifted by the same amount. Before the first move neg_m is 0 and thr
-// -inf, so the first sub-block sets the max from its own scores.
+// -inf, so the first sub-block sets the max from its own scores. The common path
+// checks each lane half's own max; the column max over both halves is formed
+// only in the rare branch.
 __device__ __forceinline__ void shift_and_check(f32x16& sv, WaveState& ws, float scale) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) sv[r] = fmaf(sv[r], scale, ws.neg_m);
+  // each lane half checks its own 8 + 8 keys; only when some lane exceeds the
+  // threshold is the column max of both halves formed
   float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
 #pragma unroll
   for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, sv[r]), sv[r + 1]);
   mx = fmaxf(mx, sv[15]);
-  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false,
-                                                   false);
-  mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-  const bool move = mx > ws.thr;
-  if (__any(move)) {
+  if (__any(mx > ws.thr)) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                     false, false);
+    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    const bool move = mx > ws.thr;
     const float d = move ? mx : 0.0f;
     // nothing is accumulated before the first move (thr -inf): O and l stay 0
     const float corr = ws.thr == -INFINITY ? 0.0f : exp2_fast(-d);
