@@ -16,7 +16,8 @@
 //     k-steps), so each lane owns one query column: the online softmax is in-lane
 //     plus one lane-half exchange, and the probabilities already sit in the B-operand
 //     layout of O^T += V^T P^T (key slot permutation of the value tiles). The running
-//     max moves only when it grows by more than 2^8 (lazy rescale).
+//     max moves only when a column's shifted score x = s * scale - m exceeds 2^8
+//     (lazy rescale); the common path checks each lane half's own max of x.
 //   * The tile's list (entries outside [0, NB) skipped, as the reference's loop
 //     never reads them usefully) is compacted into LDS once; as in the reference,
 //     only the diagonal block j == t is masked (key > query).
@@ -29,6 +30,15 @@ constexpr int kSub = 32;                   // keys per sub-block
 constexpr int kSubElems = kSub * kD2;      // 8192 bf16 = 16 KB
 constexpr int kA2Threads = 256;
 constexpr int kA2MaxBlocks = 1024;
+constexpr float kLazy = 8.0f;              // log2 headroom before a column's running max moves
+
+// acc + lo + hi of a packed bf16 pair (v_dot2_f32_bf16 with (1, 1), from assembly:
+// the compiler's dot2 builtin lowering reads the wrong register when several of
+// them are chained)
+__device__ __forceinline__ float add_bf16_pair(float acc, uint32_t pair) {
+  asm("v_dot2_f32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(pair), "s"(0x3f803f80u));
+  return acc;
+}
 
 struct Attn256Args {
   const uint16_t* q;
@@ -138,7 +148,8 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
   f32x16 o[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = f32x16{};
-  float m_used = -INFINITY;  // log2 units; equal in both lane halves (same query)
+  float neg_m = 0.0f;        // -(running max) in log2 units once set (0 before)
+  float thr = -INFINITY;     // lazy-move threshold on shifted scores (-inf before the max is set)
   float l = 0.0f;            // this half's share of the probability sum
 
   for (int s = 0; s < steps; ++s) {
@@ -168,39 +179,48 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
       __builtin_amdgcn_sched_barrier(0);
     }
 
-    float x[16];
-    float mx = -INFINITY;
-    const bool diag = j == t;
+    // x = s * scale - m (diagonal block: keys above the query at -inf); the lazy
+    // max check runs on x, per lane half, and forms the column max over both
+    // halves only in the rare branch where some lane exceeds its threshold
+    f32x16 x;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = sb * kSub + mfma32_row(r, lane);
-      float v = sc[r] * a.scale_log2;
-      if (diag && key > qr) v = -INFINITY;
-      x[r] = v;
-      mx = fmaxf(mx, v);
+    for (int r = 0; r < 16; ++r) x[r] = fmaf(sc[r], a.scale_log2, neg_m);
+    if (j == t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (sb * kSub + mfma32_row(r, lane) > qr) x[r] = -INFINITY;
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    if (mx > m_used + 8.0f) {  // lazy rescale: only when the max grows by more than 2^8
-      const float f = exp2_fast(m_used - mx);  // 0 on the first sub-block
-      l *= f;
+    float mx = fmaxf(fmaxf(x[0], x[1]), x[2]);
+#pragma unroll
+    for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, x[r]), x[r + 1]);
+    mx = fmaxf(mx, x[15]);
+    if (__any(mx > thr)) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                       false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      const bool move = mx > thr;
+      const float d = move ? mx : 0.0f;
+      // nothing is accumulated before the first move (thr -inf): O and l stay 0
+      const float corr = thr == -INFINITY ? 0.0f : exp2_fast(-d);
+      // in place (tied operands): O keeps its registers across the rare branch
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] *= f;
-      m_used = mx;
-    }
-    const float mref = m_used == -INFINITY ? 0.0f : m_used;
-    float p[16];
+        for (int r = 0; r < 16; ++r) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(o[dt][r]) : "v"(corr));
+      l *= corr;
+      neg_m -= d;
+      if (move) thr = kLazy;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      p[r] = exp2_fast(x[r] - mref);
-      l += p[r];
+      for (int r = 0; r < 16; ++r) x[r] -= d;
     }
+    // probabilities as bf16 B operands; the running sum adds the rounded values
     u32x4 pb0, pb1;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      pb0[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
-      pb1[e] = pack_bf16x2(p[8 + 2 * e], p[8 + 2 * e + 1]);
+      pb0[e] = pack_bf16x2(exp2_fast(x[2 * e]), exp2_fast(x[2 * e + 1]));
+      l = add_bf16_pair(l, pb0[e]);
+      pb1[e] = pack_bf16x2(exp2_fast(x[8 + 2 * e]), exp2_fast(x[8 + 2 * e + 1]));
+      l = add_bf16_pair(l, pb1[e]);
     }
 #pragma unroll
     for (int d2 = 0; d2 < 4; ++d2) {
@@ -238,7 +258,7 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
     }
     if (a.lse && half == 0)
       a.lse[b * a.ls_b + qrow * a.ls_s + h * a.ls_h] =
-          l > 0.0f ? (m_used + log2f(l)) * kLn2 : -INFINITY;
+          l > 0.0f ? (log2f(l) - neg_m) * kLn2 : -INFINITY;
   }
 }
 
