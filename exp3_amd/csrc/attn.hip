@@ -723,12 +723,14 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
     // full_block, spread over its steps; here at once if this item skips block u).
     auto run_full = [&](int uu, auto buf) {
       constexpr int B = decltype(buf)::value;
+      // list entries first (written before the loop): their LDS reads overlap the wait
       const int f = __builtin_amdgcn_readfirstlane(uflag[uu]);
+      const bool more = uu + 1 < nu;
+      const int jn = __builtin_amdgcn_readfirstlane(ulist[more ? uu + 1 : uu]);
       wait_tiles();
       block_sync();  // block uu visible to all; every wave is done with block uu - 1
       NextCopy nx;
-      nx.any = uu + 1 < nu;
-      const int jn = nx.any ? __builtin_amdgcn_readfirstlane(ulist[uu + 1]) : 0;
+      nx.any = more;
       nx.k = kbase + jn * tile_elems;
       nx.v = vbase + jn * tile_elems;
       nx.kd = kbuf[B ^ 1];
