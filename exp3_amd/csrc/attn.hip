@@ -75,11 +75,6 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   return row * kBlock + ((chunk ^ (row & 15)) << 3);
 }
 
-// In-row offset of element c of row `row` in a swizzled tile.
-__device__ __forceinline__ int swz_off(int row, int c) {
-  return (((c >> 3) ^ (row & 15)) << 3) + (c & 7);
-}
-
 __device__ __forceinline__ bf16x8 lds_read16(const uint16_t* lds, int off) {
   return as_bf16x8(*reinterpret_cast<const u32x4*>(lds + off));
 }
