@@ -2,17 +2,18 @@
 //
 // V1 score (upstream/flashprefill_native_forward.py:89-175 + normalize_scores
 // :410-417). One workgroup per (query tile t, q head h): four waves each hold 32
-// query rows of Q in registers as the MFMA A operand and stream the bf16 block
-// means Kbar_j (B operand, L2-resident, 256 B per block) in chunks of 32 blocks:
+// query rows of Q in registers as the MFMA A operand; the bf16 block means Kbar_j
+// (B operand, 256 B per block at D = 128) arrive in chunks of 32 blocks, each
+// copied once per workgroup into a ring of LDS slots by direct global->LDS loads
+// and read by all four waves:
 //     S[row][j] = q_row . Kbar_j          (v_mfma_f32_32x32x16_bf16, fp32 acc)
 //     x = S * fp32(scale * log2 e)
 // Row i of tile t is valid for block j iff i >= 128 (j + 1) - 1 and i < S. Each
 // lane reduces its 16 rows of one block column to (max, sum 2^(x - max)) and
-// merges with the other lane half; every wave walks all chunks on its own (the
-// next chunk's Kbar operands load while the current one is reduced) and leaves its
-// rows' partials in LDS, and after one barrier the four waves' partials are merged
-// in a fixed order, giving M_tj and m_tj. The normalisation w_j = m_tj 2^(M_tj - max_j M_tj) / (sum_j w + 1e-9)
-// runs in the same workgroup, so the raw scores never reach HBM.
+// merges with the other lane half; the four waves' partials of a chunk are merged
+// in a fixed order after the next chunk's barrier, giving M_tj and m_tj. The
+// normalisation w_j = m_tj 2^(M_tj - max_j M_tj) / (sum_j w + 1e-9) runs in the
+// same workgroup, so the raw scores never reach HBM.
 //
 // Selection (upstream :357-407 and kernels.py:129-160) is one shared device
 // routine over a score row held in LDS: threshold fp32(max * alpha), protected
@@ -150,23 +151,134 @@ struct V1Args {
   uint8_t* mask;
 };
 
-template <int D>
+// (max, mass) of one chunk column: this lane's 16 rows of block j. Rows are valid
+// for j when row_in_tile >= lim (lim = 128 (j - t) + 127, at most -1 below the
+// diagonal) and row_in_tile < rows_left. With a positive scale c the row maximum
+// is taken over the raw products, since rounding is monotone:
+// max_r fp32(acc_r c) = fp32(max_r(acc_r) c); the exponent is then one fma.
+template <bool kPosScale, bool kMasked>
+__device__ __forceinline__ void chunk_column(const f32x16& acc, float c, int lim, int rows_left,
+                                             int wave, int lane, float& mx, float& mass) {
+  bool valid[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = wave * 32 + mfma32_row(r, lane);
+    valid[r] = !kMasked || (row >= lim && row < rows_left);
+  }
+  mass = 0.0f;
+  if constexpr (kPosScale) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m = fmaxf(m, valid[r] ? acc[r] : -INFINITY);
+    mx = m * c;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float e = exp2_fast(fmaf(acc[r], c, -mx));
+        mass += valid[r] ? e : 0.0f;
+      }
+    }
+  } else {
+    float xs[16];
+    float m = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      xs[r] = valid[r] ? acc[r] * c : -INFINITY;
+      m = fmaxf(m, xs[r]);
+    }
+    mx = m;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mass += exp2_fast(xs[r] - mx);
+    }
+  }
+}
+
+// Dynamic LDS of the V1 kernel: blk_max, blk_mass [NB].
+__host__ __device__ constexpr size_t v1_lds_bytes(int blocks) { return 2u * (size_t)blocks * 4u; }
+
+// Block-mean chunks (32 blocks x D dims bf16) stream through a ring of LDS slots,
+// each copied once per workgroup by direct global->LDS loads and read by all four
+// waves as MFMA B operands; kV1Ring - 1 chunks are in flight ahead of the one
+// being reduced.
+template <int D> struct V1Ring {
+  static constexpr int kSlots = D == 128 ? 4 : 3;
+  static constexpr int kUnitsPerRow = D / 8;                  // 16-byte units of one block row
+  static constexpr int kSlotElems = 32 * D;
+  static constexpr int kCopiesPerWave = 32 * kUnitsPerRow / 64 / 4;   // D/64 loads per wave
+  static_assert(kCopiesPerWave * (kSlots - 2) == 4, "ring waits below assume 4 loads");
+};
+
+// One 16-byte unit per lane, landing at lds_byte + 16 * lane (lds_byte wave-uniform).
+// Issued from assembly: the compiler's builtin for this load makes it treat all of
+// LDS as pending and wait for every copy before the next LDS read.
+__device__ __forceinline__ void v1_copy_unit(const uint16_t* src, uint32_t lds_byte) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_byte);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m0), "v"(src)
+      : "memory");
+}
+__device__ __forceinline__ void v1_wait_ring() { asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); }
+__device__ __forceinline__ void v1_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int D, bool kPosScale>
 __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
+  using Ring = V1Ring<D>;
   constexpr int kSteps = D / 16;  // 16-dim MFMA k-steps
+  constexpr int R = Ring::kSlots;
+  // Workgroups go to the 8 XCDs round-robin by id: the k-th one on XCD x takes
+  // (batch, head) k % per_tile of tile rank x + 8 (k / per_tile), rank 0 being
+  // the heaviest (last) tile. All heads of a tile then run on one XCD, so the
+  // partial cache lines of its head-interleaved index and mask rows meet in
+  // one L2, and the tiles are still dealt heaviest first over the XCDs.
   const int per_tile = a.batch * a.q_heads;
-  const int t = a.blocks - 1 - blockIdx.x / per_tile;  // heaviest tiles first
-  const int bh = blockIdx.x % per_tile;
+  const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int rank = xcd + 8 * (k / per_tile);
+  if (rank >= a.blocks) return;  // padding of the grid to 8 tile ranks
+  const int t = a.blocks - 1 - rank;
+  const int bh = k % per_tile;
   const int b = bh / a.q_heads, h = bh % a.q_heads;
   const int g = h / (a.q_heads / a.kv_heads);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
 
-  __shared__ float blk_max[kMaxBlocks];
-  __shared__ float blk_mass[kMaxBlocks];
-  __shared__ float part_max[4][kMaxBlocks];   // per-wave (max, mass) of every block
-  __shared__ float part_mass[4][kMaxBlocks];
+  __shared__ __align__(16) uint16_t ring[R][Ring::kSlotElems];
+  __shared__ float part_max[2][4][32];   // per-wave (max, mass) of the last two chunks
+  __shared__ float part_mass[2][4][32];
   __shared__ float scratch[8];
   __shared__ int wave_counts[8];
+  extern __shared__ float v1_lds[];
+  const int nb = a.blocks;
+  float* blk_max = v1_lds;
+  float* blk_mass = v1_lds + nb;
+
+  // Slot image: 16-byte unit u of block row r at unit u ^ (r & 15), so that the
+  // operand reads below (32 rows, one unit each) are free of bank conflicts. Lane
+  // L of a wave's i-th copy fills unit P = (4 i + wave) 64 + L of the slot; block
+  // rows past the last block read the last block (masked out in the reduction).
+  const uint16_t* kb_bg = a.kbar + b * a.ms_b + g * a.ms_h;
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)&ring[0][0];
+  auto issue_chunk = [&](int jc) {
+    const uint32_t slot_lds = ring_lds + (uint32_t)((jc % R) * Ring::kSlotElems * 2);
+#pragma unroll
+    for (int i = 0; i < Ring::kCopiesPerWave; ++i) {
+      const int p0 = (i * 4 + wave) * 64;
+      const int unit = p0 + lane;
+      const int r = unit / Ring::kUnitsPerRow;
+      const int lu = (unit % Ring::kUnitsPerRow) ^ (r & 15);
+      const int j = min(jc * 32 + r, nb - 1);
+      v1_copy_unit(kb_bg + (int64_t)j * a.ms_j + lu * 8, slot_lds + (uint32_t)p0 * 16u);
+    }
+  };
+  const int nchunks = (t + 1 + 31) / 32;
+  for (int p = 0; p < R - 1 && p < nchunks; ++p) issue_chunk(p);
 
   // Q rows as A operands: lane holds row (wave * 32 + col), dims dc*16 + 8*half + 0..7.
   const int row_in_tile = wave * 32 + col;
@@ -182,57 +294,28 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
       qa[dc] = as_bf16x8(raw);
     }
   }
-  const uint16_t* kb_base = a.kbar + b * a.ms_b + g * a.ms_h + half * 8;
-  auto load_kbar = [&](int jc, bf16x8 (&kb)[kSteps]) {
-    const int j = jc * 32 + col;
-    const bool ok = j < a.blocks;
+
+  const float c = a.scale_log2;
+  const int rows_left = a.seq - t * kBlock;               // valid rows of tile t (<= 128)
+  const bool tile_full = rows_left >= kBlock;
+  // this lane's operand unit for k-step dc is (2 dc + half) ^ (col & 15) = 2 dc ^ hc
+  const int hc = half ^ (col & 15);
+  auto process = [&](int jc) {
+    const uint16_t* slot = &ring[jc % R][col * D];
+    f32x16 acc = {};
 #pragma unroll
     for (int dc = 0; dc < kSteps; ++dc) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (ok) raw = *reinterpret_cast<const u32x4*>(kb_base + (int64_t)j * a.ms_j + dc * 16);
-      kb[dc] = as_bf16x8(raw);
-    }
-  };
-
-  // Each wave walks every chunk of 32 blocks on its own (no barrier inside the
-  // loop; the next chunk's Kbar operands load while this one is reduced) and
-  // leaves its 32 rows' (max, mass) per block in LDS; the four waves merge after.
-  // (prefetch at D = 128 only: at D = 256 the second operand set costs occupancy)
-  constexpr bool kPrefetch = D == 128;
-  const int nchunks = (t + 1 + 31) / 32;
-  bf16x8 kb_next[kSteps];
-  if (kPrefetch && nchunks > 0) load_kbar(0, kb_next);
-  for (int jc = 0; jc < nchunks; ++jc) {
-    const int j = jc * 32 + col;  // this lane's block column
-    f32x16 acc = {};
-    {
-      bf16x8 kb[kSteps];
-      if (kPrefetch) {
-#pragma unroll
-        for (int dc = 0; dc < kSteps; ++dc) kb[dc] = kb_next[dc];
-        if (jc + 1 < nchunks) load_kbar(jc + 1, kb_next);
-      } else {
-        load_kbar(jc, kb);
-      }
-#pragma unroll
-      for (int dc = 0; dc < kSteps; ++dc) acc = mfma32(qa[dc], kb[dc], acc);
+      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(slot + ((2 * dc) ^ hc) * 8);
+      acc = mfma32(qa[dc], kb, acc);
     }
     // acc[r] = S[row 8*(r/4) + 4*half + r%4 of this wave][block j]
-    const int64_t key_end = (int64_t)(j + 1) * kBlock - 1;
-    float xs[16];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t i = (int64_t)t * kBlock + wave * 32 + mfma32_row(r, lane);
-      const bool valid = i >= key_end && i < a.seq;
-      const float x = acc[r] * a.scale_log2;
-      xs[r] = valid ? x : -INFINITY;
-      mx = fmaxf(mx, xs[r]);
-    }
-    float mass = 0.0f;
-    if (mx != -INFINITY) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mass += exp2_fast(xs[r] - mx);
+    const int j = jc * 32 + col;  // this lane's block column
+    float mx, mass;
+    if (tile_full && jc * 32 + 31 < t) {
+      chunk_column<kPosScale, false>(acc, c, 0, kBlock, wave, lane, mx, mass);
+    } else {
+      chunk_column<kPosScale, true>(acc, c, kBlock * (j - t) + kBlock - 1, rows_left, wave,
+                                    lane, mx, mass);
     }
     // merge the two lane halves (rows 4*half + ...)
     {
@@ -246,25 +329,46 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
       mx = nm;
       mass = merged;
     }
-    if (half == 0 && j < a.blocks) {
-      part_max[wave][j] = mx;
-      part_mass[wave][j] = mass;
+    if (half == 0) {
+      part_max[jc & 1][wave][col] = mx;
+      part_mass[jc & 1][wave][col] = mass;
     }
+  };
+  // the four waves' partials of chunk jc -> blk_max / blk_mass (threads 0..31)
+  auto merge_chunk = [&](int jc) {
+    const int jj = jc * 32 + tid;
+    if (tid < 32 && jj < nb) {
+      float m = part_max[jc & 1][0][tid];
+      for (int w = 1; w < 4; ++w) m = fmaxf(m, part_max[jc & 1][w][tid]);
+      float s2 = 0.0f;
+      if (m != -INFINITY) {
+        for (int w = 0; w < 4; ++w) {
+          const float pm = part_max[jc & 1][w][tid];
+          if (pm != -INFINITY) s2 += part_mass[jc & 1][w][tid] * exp2_fast(pm - m);
+        }
+      }
+      blk_max[jj] = m;
+      blk_mass[jj] = s2;
+    }
+  };
+  // Q is consumed here, so the compiler's wait for it (which also covers the
+  // first copies) sits before the loop rather than inside it.
+#pragma unroll
+  for (int dc = 0; dc < kSteps; ++dc) asm volatile("" ::"v"(qa[dc]));
+
+  // One barrier per chunk: after it, chunk jc is in LDS for every wave, every wave
+  // is done reading the slot the next copy overwrites, and the partials of chunk
+  // jc - 1 are complete.
+  for (int jc = 0; jc < nchunks; ++jc) {
+    if (jc + R - 2 < nchunks) v1_wait_ring();   // chunks jc + 1 .. jc + R - 2 may stay in flight
+    else v1_wait_all();
+    block_sync();
+    if (jc > 0) merge_chunk(jc - 1);
+    if (jc + R - 1 < nchunks) issue_chunk(jc + R - 1);
+    process(jc);
   }
   block_sync();
-  for (int jj = tid; jj < min(nchunks * 32, a.blocks); jj += kRouteThreads) {
-    float m = part_max[0][jj];
-    for (int w = 1; w < 4; ++w) m = fmaxf(m, part_max[w][jj]);
-    float s2 = 0.0f;
-    if (m != -INFINITY) {
-      for (int w = 0; w < 4; ++w) {
-        const float pm = part_max[w][jj];
-        if (pm != -INFINITY) s2 += part_mass[w][jj] * exp2_fast(pm - m);
-      }
-    }
-    blk_max[jj] = m;
-    blk_mass[jj] = s2;
-  }
+  if (nchunks > 0) merge_chunk(nchunks - 1);
   block_sync();
 
   // normalize_scores over j <= t; j > t has M = -inf and contributes 0.
@@ -425,6 +529,24 @@ static int v1_common(const void* q, const int64_t* q_strides, const void* mean_k
   return SPX_OK;
 }
 
+// One workgroup per (query tile, batch, q head), the tile count padded to a
+// multiple of 8 (the XCD count); LDS sized to the block count (at most 40 KB at
+// 1024 blocks). A positive scale takes the row maxima over the raw products; any
+// other scale (zero, negative, NaN) scales every product first.
+static void launch_v1(const V1Args& a, int head_dim, void* stream) {
+  const int grid = 8 * ((a.blocks + 7) / 8) * a.batch * a.q_heads;
+  const size_t lds = v1_lds_bytes(a.blocks);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool pos = a.scale_log2 > 0.0f;
+  if (head_dim == 128) {
+    if (pos) v1_route_kernel<128, true><<<grid, kRouteThreads, lds, st>>>(a);
+    else v1_route_kernel<128, false><<<grid, kRouteThreads, lds, st>>>(a);
+  } else {
+    if (pos) v1_route_kernel<256, true><<<grid, kRouteThreads, lds, st>>>(a);
+    else v1_route_kernel<256, false><<<grid, kRouteThreads, lds, st>>>(a);
+  }
+}
+
 extern "C" int spx_v1_scores(const void* q, const int64_t* q_strides, const void* mean_k,
                              const int64_t* mean_k_strides, int batch, int seq, int q_heads,
                              int kv_heads, int head_dim, int block_size, float scale,
@@ -437,11 +559,7 @@ extern "C" int spx_v1_scores(const void* q, const int64_t* q_strides, const void
   a.score = score;
   a.ss_b = score_strides[0]; a.ss_t = score_strides[1]; a.ss_j = score_strides[2];
   a.ss_h = score_strides[3];
-  const int grid = a.blocks * batch * q_heads;
-  if (head_dim == 128)
-    v1_route_kernel<128><<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
-  else
-    v1_route_kernel<256><<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  launch_v1(a, head_dim, stream);
   return launch_status("v1_scores");
 }
 
@@ -469,11 +587,7 @@ extern "C" int spx_v1_route(const void* q, const int64_t* q_strides, const void*
   a.indices = indices;
   a.counts = counts;
   a.mask = mask;
-  const int grid = a.blocks * batch * q_heads;
-  if (head_dim == 128)
-    v1_route_kernel<128><<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
-  else
-    v1_route_kernel<256><<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  launch_v1(a, head_dim, stream);
   return launch_status("v1_route");
 }
 
