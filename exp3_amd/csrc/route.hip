@@ -206,7 +206,8 @@ template <int D> struct V1Ring {
   static constexpr int kUnitsPerRow = D / 8;                  // 16-byte units of one block row
   static constexpr int kSlotElems = 32 * D;
   static constexpr int kCopiesPerWave = 32 * kUnitsPerRow / 64 / 4;   // D/64 loads per wave
-  static_assert(kCopiesPerWave * (kSlots - 2) == 4, "ring waits below assume 4 loads");
+  static constexpr int kInFlight = kCopiesPerWave * (kSlots - 2);      // loads left after a chunk's wait
+  static_assert(kInFlight == 2 || kInFlight == 4, "ring waits below cover 2 or 4 loads");
 };
 
 // One 16-byte unit per lane, landing at lds_byte + 16 * lane (lds_byte wave-uniform).
@@ -225,7 +226,10 @@ __device__ __forceinline__ void v1_copy_unit(const uint16_t* src, uint32_t lds_b
       : "s"(m0), "v"(src)
       : "memory");
 }
-__device__ __forceinline__ void v1_wait_ring() { asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); }
+template <int N> __device__ __forceinline__ void v1_wait_ring() {
+  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+}
 __device__ __forceinline__ void v1_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 template <int D, bool kPosScale>
@@ -360,7 +364,7 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   // is done reading the slot the next copy overwrites, and the partials of chunk
   // jc - 1 are complete.
   for (int jc = 0; jc < nchunks; ++jc) {
-    if (jc + R - 2 < nchunks) v1_wait_ring();   // chunks jc + 1 .. jc + R - 2 may stay in flight
+    if (jc + R - 2 < nchunks) v1_wait_ring<Ring::kInFlight>();   // chunks jc + 1 .. jc + R - 2 stay in flight
     else v1_wait_all();
     block_sync();
     if (jc > 0) merge_chunk(jc - 1);
