@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from exp3_amd import kernels, synthetic
+from exp3_amd import attention, kernels, synthetic
 from exp3_amd.upstream import flashprefill_native_forward as up
 from oracle import reference_cpu as ref
 from tests.helpers import (SCALE, assert_output_close, inputs, masks_equal_except_ties,
@@ -94,6 +94,38 @@ def test_v1_scores(gpu, length):
     assert np.all(np.isclose(rows, 1.0, atol=1e-5) | np.isclose(rows, 0.0, atol=1e-9))
     upper = np.triu(np.ones((actual.shape[1],) * 2, dtype=bool), k=1)
     assert (actual[:, upper] == 0).all()
+
+
+@pytest.mark.parametrize("scale", (-SCALE, 0.0))
+def test_v1_route_non_positive_scale(gpu, scale):
+    """The route kernel's path for a scale that is not positive (every product is
+    scaled before the maximum; a positive scale takes the maximum over the raw
+    products): V1 scores against the oracle, the fused route's mask equal to the
+    selection rule on its own scores, and its lists equal to that mask's. At scale
+    0 every valid row has x = 0, so a block's score is its count of valid rows over
+    the tile's total (a closed form)."""
+    length, alpha = 1089, 0.3
+    q, k, v = inputs(length, seed=13)
+    qg, kg, vg = _gpu(q, k, v)
+    backend = attention.AttentionBackend(alpha=alpha, register=False)
+    backend.configure("fp_v1", alpha)
+    record = {"events": {}}
+    _, kbar, scores, idx, cnt, sel = backend._v1_selection(qg, kg, scale, record, vg, True)
+    g_scores = to_np(scores)
+    expected = ref.v1_scores(to_np(q), to_np(kbar), scale)
+    np.testing.assert_allclose(g_scores, expected, atol=2e-4, rtol=0.005)
+    if scale == 0.0:
+        blocks = ref.num_blocks(length)
+        rows = np.arange(length)
+        valid = rows[:, None] >= (np.arange(blocks)[None, :] + 1) * 128 - 1      # [S, NB]
+        per_tile = np.add.reduceat(valid.astype(np.float64), np.arange(0, length, 128), axis=0)
+        closed = per_tile / (per_tile.sum(axis=1, keepdims=True) + 1e-9)
+        np.testing.assert_allclose(g_scores[0, :, :, 0], closed, atol=1e-6, rtol=1e-5)
+    own = ref.mask_from_indices(*ref.deal_output_score(g_scores, 2, 4, alpha, 2, 0))
+    np.testing.assert_array_equal(to_np(sel), own)
+    e_idx, e_cnt = ref.indices_from_mask(to_np(sel))
+    np.testing.assert_array_equal(to_np(idx), e_idx)
+    np.testing.assert_array_equal(to_np(cnt), e_cnt)
 
 
 def _adversarial_scores(length, seed):
