@@ -221,6 +221,8 @@ class AttentionBackend:
         common_tail = (batch, sequence, q_heads, k.shape[2], head_dim, self.block_size,
                        float(scale), _lib.ptr(output), _lib.strides(output), _lib.ptr(lse),
                        _lib.strides(lse), _lib.stream(device))
+        if head_dim in upstream._ATTENTION_CONFIGS:   # what attention_tile_sizes() reports
+            upstream._flash_forward.best_config = upstream._ATTENTION_CONFIGS[head_dim]
         events = None
         if self.kernel_events is not None:
             events = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))

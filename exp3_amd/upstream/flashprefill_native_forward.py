@@ -22,6 +22,46 @@ ATTENTION_K_TILE = 128   # keys per LDS tile
 SCORE_K_TILE = 32        # key blocks per score MFMA chunk
 
 
+class LaunchConfig:
+    """What a Triton autotuner's ``best_config`` exposes (``kwargs``,
+    ``num_warps``, ``num_stages``), describing a fixed HIP launch: ``num_warps``
+    is wavefronts (64 lanes) per workgroup, ``num_stages`` the LDS buffers a key
+    tile streams through."""
+
+    def __init__(self, num_warps: int, num_stages: int, **kwargs):
+        self.kwargs = dict(kwargs)
+        self.num_warps = num_warps
+        self.num_stages = num_stages
+
+    def __repr__(self):
+        return (f"LaunchConfig({self.kwargs}, num_warps={self.num_warps}, "
+                f"num_stages={self.num_stages})")
+
+
+class KernelInfo:
+    """Stand-in for a reference Triton kernel object, read only for its
+    ``best_config`` (check_qwen35_math.py:134-139, upstream :524-533)."""
+
+    def __init__(self, name: str, best_config: LaunchConfig):
+        self.__name__ = name
+        self.best_config = best_config
+
+
+# head dim -> attention kernel geometry: d = 128 runs two 128-row query tiles per
+# 8-wave workgroup over 128-key tiles (double-buffered); d = 256 one tile per
+# 4-wave workgroup over 32-key sub-blocks (double-buffered)
+_ATTENTION_CONFIGS = {
+    128: LaunchConfig(8, 2, Q_TILE_SIZE=ATTENTION_Q_TILE, K_TILE_SIZE=ATTENTION_K_TILE),
+    256: LaunchConfig(4, 2, Q_TILE_SIZE=ATTENTION_Q_TILE, K_TILE_SIZE=32),
+}
+
+# ``best_config`` follows the head dim of the last exact_attention launch (d = 128
+# until a d = 256 launch), as the reference's reflects its last autotuned launch.
+_flash_forward = KernelInfo("attn_kernel", _ATTENTION_CONFIGS[128])
+compute_block_score = KernelInfo(
+    "v1_route_kernel", LaunchConfig(4, 4, Q_TILE_SIZE=128, K_TILE_SIZE=SCORE_K_TILE))
+
+
 def _blocks(sequence: int, block_size: int) -> int:
     return (sequence + block_size - 1) // block_size
 
@@ -124,6 +164,8 @@ def exact_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     batch, sequence, q_heads, head_dim = q.shape
     check_attention_shapes(q, k, v, indices, counts, block_size)
     key_tiles, value_tiles = attention_tiles(k, v, block_size)
+    if head_dim in _ATTENTION_CONFIGS:
+        _flash_forward.best_config = _ATTENTION_CONFIGS[head_dim]
     output = torch.empty(batch, sequence, q_heads, head_dim, dtype=q.dtype, device=device)
     lse = torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
     _lib.call("spx_exact_attention", _lib.ptr(q), _lib.strides(q), _lib.ptr(key_tiles),
@@ -154,9 +196,10 @@ def check_attention_shapes(q, k, v, indices, counts, block_size=128):
 
 def attention_tile_sizes():
     """(query tile, key tile) of the attention kernel (upstream :524-528)."""
-    return ATTENTION_Q_TILE, ATTENTION_K_TILE
+    config = _flash_forward.best_config
+    return config.kwargs["Q_TILE_SIZE"], config.kwargs["K_TILE_SIZE"]
 
 
 def score_tile_size():
     """Key blocks per score MFMA chunk (upstream :531-533)."""
-    return SCORE_K_TILE
+    return compute_block_score.best_config.kwargs["K_TILE_SIZE"]

@@ -2,15 +2,15 @@
 reduction that ``bench.py`` reports as ``roofline.traffic``.
 
 Workloads (run as the program after ``rocprofv3 ... --``):
-  python -m exp3_amd.profiling attention [--seq 32640] [--method mean_native] [--repeats 2]
+  python -m measure.profiling attention [--seq 32640] [--method mean_native] [--repeats 2]
                                          [--q-heads 28 --kv-heads 4 --head-dim 128] [--dense-impl sdpa]
       one prefill attention layer (pool, route, attention) per repeat, as bench.py runs it
-  python -m exp3_amd.profiling copy [--gib 1]
+  python -m measure.profiling copy [--gib 1]
       a plain device copy of known size (torch copy_), the calibration for the
       FETCH_SIZE / WRITE_SIZE counters
 
 Reduction:
-  python -m exp3_amd.profiling traffic --attn-fetch DIR --attn-write DIR \
+  python -m measure.profiling traffic --attn-fetch DIR --attn-write DIR \
       --copy-fetch DIR --copy-write DIR [--copy-gib 1] [--key mean_native:32640] \
       [--out profiles/hbm_traffic.json]
       reads the counter_collection CSVs of four ``rocprofv3 --pmc FETCH_SIZE`` /

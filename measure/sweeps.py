@@ -1,24 +1,24 @@
 """Measurement runs beyond the headline bench line (one GPU, synthetic data).
 
-  python -m exp3_amd.sweeps needles [--seq 32640] [--needles 64]
+  python -m measure.sweeps needles [--seq 32640] [--needles 64]
       planted-retrieval inputs; alpha in {0.04, 0.08, 0.16} for the four mean
       methods, fp_v1 at 0.08 and dense: ms/layer, selected-block density
       counts.sum() / (H NB (NB + 1) / 2) and the exact-pair ratio
       (kernels.py:338-353 accounting)
-  python -m exp3_amd.sweeps long [--seq 131072] [--needles 256]
+  python -m measure.sweeps long [--seq 131072] [--needles 256]
       long context: cgf_mean and dispersion_mean at alpha 0.04 (plus mean_native
       at 0.04 for reference), same columns
-  python -m exp3_amd.sweeps sparse [--seq 32640] [--qk-scale 4]
+  python -m measure.sweeps sparse [--seq 32640] [--qk-scale 4]
       sparse selections (not a BASELINE config): the seeded inputs with Q and K
       multiplied by --qk-scale (bf16) sharpen the block scores, and alpha in
       {0.08, 0.3, 0.5, 0.7} gives densities well below 1, exercising the block-mean
       and rescue tails; mean_native, fp_v1, cgf_mean, fp_v1_rescue_v2 and dense
-  python -m exp3_amd.sweeps d256 [--seq 32640]
+  python -m measure.sweeps d256 [--seq 32640]
       head_dim 256 with 16 query / 4 KV heads (Qwen3.5 full-attention layer shape,
       check_qwen35_math.py): dense (torch SDPA and the HIP kernel) and fp_v1 at
       alpha 0.08; ms/layer, the attention kernel's HIP-event time and its rate over
       the selected 128 x 128 tiles (4 x 128 x 128 x 256 FLOP each)
-  python -m exp3_amd.sweeps model [--seq 32640] [--layers 28] [--repeats 3]
+  python -m measure.sweeps model [--seq 32640] [--layers 28] [--repeats 3]
       full prefill of a random-init Qwen2.5-7B-shaped model built from a local
       config (28 layers, hidden 3584, FFN 18944, 28/4 heads, RMSNorm 1e-6,
       theta 1e6, vocab 152064, QKV bias, bf16) with the attention backend

@@ -85,6 +85,12 @@ def test_reference_interface():
     b.configure("fp_v1", 0.16)
     assert (b.method, b.alpha) == ("fp_v1", 0.16)
     assert up.attention_tile_sizes() == (128, 128) and up.score_tile_size() == 32
+    # check_qwen35_math.py:134-139 reads the exact-attention launch through
+    # _flash_forward.best_config; attention_tile_sizes() reports the same values
+    config = up._flash_forward.best_config
+    launch = {**config.kwargs, "num_warps": config.num_warps, "num_stages": config.num_stages}
+    assert launch == {"Q_TILE_SIZE": 128, "K_TILE_SIZE": 128, "num_warps": 8, "num_stages": 2}
+    assert up.compute_block_score.best_config.kwargs["K_TILE_SIZE"] == up.score_tile_size()
     with pytest.raises(ValueError, match="unsupported selector"):
         kernels.selector_scores(torch.zeros(1, 8, 1, 128), None, 0.1, "bogus")
     with pytest.raises(ValueError, match="ROCm GPU"):

@@ -6,7 +6,7 @@ import json
 
 import pytest
 
-from exp3_amd import profiling
+from measure import profiling
 
 
 def _counter_csv(directory, rows):
@@ -54,7 +54,7 @@ def test_traffic_reduction_scales_by_copy_calibration(tmp_path):
 def test_qwen2_7b_config_matches_the_model_shape():
     torch = pytest.importorskip("torch")
     transformers = pytest.importorskip("transformers")
-    from exp3_amd import sweeps
+    from measure import sweeps
     cfg = sweeps.qwen2_7b_config(28)
     assert (cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers) == (3584, 18944, 28)
     assert (cfg.num_attention_heads, cfg.num_key_value_heads, cfg.vocab_size) == (28, 4, 152064)

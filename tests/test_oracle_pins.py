@@ -117,6 +117,23 @@ def test_v1_scores_against_check_math_reference(length):
     assert (got[:, upper] == 0).all()
 
 
+@pytest.mark.parametrize("length", (1, 100, 127))
+def test_v1_scores_without_valid_rows_are_zero(length):
+    """normalize_scores' ``+ 1e-9`` (upstream :410-417): a sequence shorter than
+    one block has no valid row for any key block (rows i >= 127 only), so every
+    weight is 0 and the score is 0 / (0 + 1e-9) = 0, not 0 / 0."""
+    q = rnd((1, length, 2, 16), 8)
+    kbar = ref.block_mean_k(rnd((1, length, 1, 16), 9))
+    mass, maximum = ref.v1_scores_raw(q, kbar, SCALE)
+    assert (maximum == -np.inf).all() and (mass == 0).all()
+    got = ref.v1_scores(q, kbar, SCALE)
+    assert np.isfinite(got).all() and (got == 0).all()
+    # the same for a row of the normaliser fed directly: no finite maximum
+    direct = ref.normalize_scores(np.zeros((1, 2, 2, 1), np.float32),
+                                  np.full((1, 2, 2, 1), -np.inf, np.float32))
+    assert np.isfinite(direct).all() and (direct == 0).all()
+
+
 def test_v1_raw_diagonal_uses_last_row_only():
     q = rnd((1, 300, 2, 16), 6)
     kbar = ref.block_mean_k(rnd((1, 300, 1, 16), 7))
