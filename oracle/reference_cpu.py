@@ -308,7 +308,8 @@ def mask_from_indices(indices: np.ndarray, counts: np.ndarray) -> np.ndarray:
 # -------------------------------------------------------------- new selectors
 
 def selector_scores(q: np.ndarray, descriptors: BlockDescriptors, scale: float,
-                    selector: str, block_size: int = BLOCK_SIZE, precision: str = "f64"):
+                    selector: str, block_size: int = BLOCK_SIZE, precision: str = "f64",
+                    tiles=None):
     """Balanced / CGF / dispersion block scores (kernels.py:49-126).
 
     Per real row r of tile t and head h, over visible blocks j < t:
@@ -316,6 +317,9 @@ def selector_scores(q: np.ndarray, descriptors: BlockDescriptors, scale: float,
     logits = l0 (balanced) or l0 + u / 2 (cgf, dispersion); p = softmax_j;
     contribution = p, or p * sqrt(u) * sigma_V (dispersion); score[t, j] is the
     mean of the contributions over the tile's real rows (0 for j >= t).
+    ``tiles`` restricts the work to the rows of the given query tiles: a tile's
+    scores depend only on its own rows, so those tiles' scores are exact and the
+    other tiles' stay 0.
     """
     if selector not in SELECTORS:
         raise ValueError(f"unsupported selector: {selector}")
@@ -324,15 +328,20 @@ def selector_scores(q: np.ndarray, descriptors: BlockDescriptors, scale: float,
     blocks = descriptors.mean_k.shape[1]
     group = q_heads // descriptors.mean_k.shape[2]
     log_counts = np.log(descriptors.counts.astype(np.float32)).astype(acc)
-    row_tiles = np.arange(sequence) // block_size
-    visible = np.arange(blocks)[None, :] < row_tiles[:, None]          # [S, NB]
+    rows = np.arange(sequence)
+    if tiles is not None:
+        rows = np.concatenate([np.arange(t * block_size, min(sequence, (t + 1) * block_size))
+                               for t in sorted(set(tiles))])
+    row_tiles = rows // block_size
+    visible = np.arange(blocks)[None, :] < row_tiles[:, None]          # [rows, NB]
     tile_rows = np.bincount(row_tiles, minlength=blocks).astype(acc)
+    tile_rows = np.where(tile_rows > 0, tile_rows, 1)
     scores = np.zeros((batch, blocks, blocks, q_heads), dtype=np.float32)
     with np.errstate(invalid="ignore", divide="ignore", over="ignore"):
         for b in range(batch):
             for h in range(q_heads):
                 g = h // group
-                query = q[b, :, h].astype(acc)
+                query = q[b, rows, h].astype(acc)
                 ell0 = query @ descriptors.mean_k[b, :, g].astype(acc).T * acc(scale)
                 ell0 = ell0 + log_counts[None, :]
                 if selector == "mean_balanced":
@@ -678,15 +687,31 @@ def attention_layer(q, k, v, scale, method, alpha=0.08, sink=2, window=4, last=2
             scores = selector_scores(q, descriptors, scale, method, block_size, precision)
         selected = protected_selection(scores, alpha, sink, window, last)
         indices, counts = indices_from_mask(selected)
+    out, lse = attention_from_selection(q, k, v, scale, method, selected, descriptors,
+                                        block_size=block_size, precision=precision, tiles=tiles)
+    result.update(output=out, lse=lse, scores=scores, indices=indices, counts=counts,
+                  selected=selected)
+    return result
+
+
+def attention_from_selection(q, k, v, scale, method, selected, descriptors=None, choice=None,
+                             block_size: int = BLOCK_SIZE, precision: str = "f64", tiles=None):
+    """The attention half of a prefill call (attention.py:253-333) for a given
+    selection mask: exact attention over ``indices_from_mask(selected)``, then the
+    block-mean tail + merge (mean methods; ``descriptors`` computed when None) or
+    the rescue tail + merge (rescue methods; ``choice`` computed when None).
+    Returns (output, LSE); ``tiles`` restricts the work to those query tiles."""
+    indices, counts = indices_from_mask(selected)
     out, lse = exact_attention(q, k, v, indices, counts, scale, block_size, precision, tiles)
     if method in MEAN_METHODS:
-        mean_out, mean_lse = mean_tail(q, descriptors, selected, scale, block_size, precision)
+        if descriptors is None:
+            descriptors = block_descriptors(k, v, block_size, precision)
+        mean_out, mean_lse = mean_tail(q, descriptors, selected, scale, block_size, precision,
+                                       tiles=tiles)
         out, lse = merge_exact_mean(out, lse, mean_out, mean_lse)
     elif method in RESCUE_METHODS:
         r_out, r_lse = rescue_tail(q, k, v, selected, scale, block_size,
                                    remainder=method == "fp_v1_rescue_v2", precision=precision,
-                                   tiles=tiles)
+                                   tiles=tiles, choice=choice)
         out, lse = merge_exact_mean(out, lse, r_out, r_lse)
-    result.update(output=out, lse=lse, scores=scores, indices=indices, counts=counts,
-                  selected=selected)
-    return result
+    return out, lse

@@ -59,3 +59,63 @@ def masks_equal_except_ties(actual, expected, ties):
     unexplained = differ & ~ties
     return int(unexplained.sum()), int(differ.sum()), [tuple(int(x) for x in idx)
                                                       for idx in np.argwhere(differ & ties)[:20]]
+
+
+# ------------------------------------------------------ whole-layer comparisons
+
+V1_METHODS = ("fp_v1", "mean_native", "fp_v1_rescue", "fp_v1_rescue_v2")
+SELECTOR_METHODS = ("mean_balanced", "cgf_mean", "dispersion_mean")
+
+
+def gpu_routing(backend, qg, kg, vg, method, scale=SCALE):
+    """The GPU's scores (float32 numpy) and selection mask for ``method``, from the
+    same kernels ``forward`` launches (every stage is deterministic)."""
+    from exp3_amd import kernels
+    record = {"events": {}}
+    if method in V1_METHODS:
+        values = vg if method in ("mean_native", "fp_v1_rescue_v2") else None
+        _, _, scores, _, _, sel = backend._v1_selection(qg, kg, scale, record, values, True)
+    else:
+        desc, _, _, _, sel = backend._new_selection(qg, kg, vg, scale, record)
+        scores = kernels.selector_scores(qg, desc, scale, method)
+    return to_np(scores), to_np(sel)
+
+
+def oracle_scores(qn, kn, vn, method, scale=SCALE, tiles=None):
+    """The oracle's routing scores (float32 arithmetic, as the reference's)."""
+    if method in V1_METHODS:
+        kbar = ref.block_mean_k(kn, precision="f32")
+        return ref.v1_scores(qn, kbar, scale, precision="f32")
+    desc = ref.block_descriptors(kn, vn, precision="f32")
+    return ref.selector_scores(qn, desc, scale, method, precision="f32", tiles=tiles)
+
+
+def select(scores, method, alpha):
+    """The reference's selection rule for ``method`` applied to ``scores``."""
+    if method in V1_METHODS:
+        return ref.mask_from_indices(*ref.deal_output_score(scores, 2, 4, alpha, 2, 0))
+    return ref.protected_selection(scores, alpha, 2, 4, 2)
+
+
+def agreeing_tiles(wanted, actual_sel, expected_sel, reach=4):
+    """Each wanted query tile, or the nearest one within ``reach`` whose masks
+    (every head) agree; a tile whose selection differs at a threshold tie would
+    compare two different attention problems."""
+    blocks = actual_sel.shape[1]
+    same = (actual_sel == expected_sel).all(axis=(0, 2, 3))
+    chosen = []
+    for t in wanted:
+        for d in range(reach + 1):
+            hit = next((c for c in (t - d, t + d) if 0 <= c < blocks and same[c]), None)
+            if hit is not None:
+                if hit not in chosen:
+                    chosen.append(hit)
+                break
+        else:
+            raise AssertionError(f"no tile near {t} with identical masks")
+    return chosen
+
+
+def tile_rows(tiles, sequence, block_size=128):
+    return np.concatenate([np.arange(t * block_size, min(sequence, (t + 1) * block_size))
+                           for t in tiles])

@@ -145,8 +145,34 @@ def test_fp_v1_route_and_layer_vs_oracle(gpu, length):
     _, _, _, _, _, _, sel = backend._route_v1(qg, kg, vg, SCALE, record, False, False)
     mism = (to_np(sel) != expected["selected"]).sum()
     assert mism <= max(2, expected["selected"].size // 5000)   # threshold ties only
+    # always compared: the oracle layer given the GPU's own selection
+    want, _ = ref.attention_from_selection(to_np(q), to_np(k), to_np(v), SCALE, "fp_v1",
+                                           to_np(sel), precision="f32")
+    assert_output_close(to_np(out), want, what="d256 fp_v1 layer")
     if mism == 0:
-        assert_output_close(to_np(out), expected["output"], what="d256 fp_v1 layer")
+        np.testing.assert_array_equal(want, expected["output"])
+
+
+def test_v1_route_ring_wraps_vs_oracle(gpu):
+    """12500 tokens = 98 blocks: the route kernel streams block means in four
+    32-block chunks through its 3-slot LDS ring at d = 256, so slots are reused
+    and partial sums merged across chunks. Scores against the oracle; the fused
+    mask and lists against the selection rule on the kernel's own scores."""
+    length, alpha = 12500, 0.08
+    q, k, v = qkv(length, seed=19)
+    qg, kg = q.cuda(), k.cuda()
+    mean_k = up.block_mean_k(kg)
+    backend = attention.AttentionBackend(alpha=alpha, register=False)
+    record = {"events": {}}
+    _, kbar, scores, idx, cnt, sel = backend._v1_selection(qg, kg, SCALE, record, None, True)
+    assert torch.equal(kbar, mean_k)
+    s = to_np(scores)
+    np.testing.assert_allclose(s, ref.v1_scores(to_np(q), to_np(kbar), SCALE, precision="f32"),
+                               atol=3e-4, rtol=0.008)   # check_qwen35_math tolerances
+    e_idx, e_cnt = ref.deal_output_score(s, 2, 4, alpha, 2, 0)
+    np.testing.assert_array_equal(to_np(idx), e_idx)
+    np.testing.assert_array_equal(to_np(cnt), e_cnt)
+    np.testing.assert_array_equal(to_np(sel), ref.mask_from_indices(e_idx, e_cnt))
 
 
 def test_dense_hip_vs_reference(gpu):
