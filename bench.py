@@ -19,6 +19,10 @@ Also reported on the same line:
   methods       ms/layer and selected-block density of all eight methods (the six of
                 the headline table plus fp_v1_rescue and fp_v1_rescue_v2);
   stages        per-stage kernel times with their roofline fractions;
+  full_model    the metric's second half: random-init Qwen2.5-7B (28 layers) prefill of
+                32640 ids, median of rotated repeats as evaluate.py times it, for dense
+                (torch SDPA under the reference's backend pin), fp_v1, mean_native and
+                dense through the HIP kernel;
   cpu_baseline  the CPU oracle (numpy restatement of the reference path) on a
                 bounded sample of the same workload, scaled to ms per layer; plus
                 BASELINE config 1 (S=4096) through the oracle in full beside the same
@@ -64,6 +68,9 @@ def parse_args():
     p.add_argument("--cpu-all-methods", action="store_true",
                    help="also time the CPU oracle for every method (several minutes)")
     p.add_argument("--traffic-file", default=str(ROOT / "profiles" / "hbm_traffic.json"))
+    p.add_argument("--no-full-model", action="store_true",
+                   help="skip the full-model 32K prefill (second half of the metric)")
+    p.add_argument("--model-repeats", type=int, default=3)
     return p.parse_args()
 
 
@@ -211,6 +218,50 @@ def _oracle_tiles(ref, qn, kn, vn, scale, method, route, tiles):
     return out
 
 
+def full_model_prefill(seq, alpha, seed, repeats, probe, torch):
+    """Second half of the metric ("full-model prefill ms"):
+    random-init Qwen2.5-7B (28 layers, bf16) prefilling ``seq`` seeded token ids with
+    the backend registered as transformers' "sdpa" attention, timed as the
+    reference's evaluate.py:323-345 / 630-663 (warm-up per case, ``repeats``
+    rotated rounds, median) inside the SDPA backend pin of evaluate.py:630.
+    Cases: dense through torch SDPA (the reference's dense), fp_v1 and mean_native
+    at ``alpha``, and dense through the HIP attention kernel (like for like)."""
+    from exp3_amd import attention
+    from measure import sweeps
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    saved = ALL_ATTENTION_FUNCTIONS["sdpa"]
+    context, sdpa_name = sweeps.dense_sdpa_context(probe)
+    backend = attention.AttentionBackend(alpha=alpha)   # registers as "sdpa"
+    try:
+        t0 = time.perf_counter()
+        model = sweeps.build_qwen2_7b(28, seed)
+        build_s = time.perf_counter() - t0
+        ids = sweeps.prompt_ids(seq, seed, model.config.vocab_size)
+        cases = [("dense", "dense", "sdpa"), ("fp_v1", "fp_v1", "sdpa"),
+                 ("mean_native", "mean_native", "sdpa"), ("dense_hip", "dense", "hip")]
+        times, tokens = sweeps.time_prefills(model, backend, ids, cases, repeats, alpha, context)
+    finally:
+        ALL_ATTENTION_FUNCTIONS["sdpa"] = saved
+    med = {label: sweeps.median(v) for label, v in times.items()}
+    result = {
+        "seq": seq, "layers": 28, "model": "random-init Qwen2.5-7B architecture, bf16",
+        "alpha": alpha, "repeats": repeats, "median_of": "rotated repeats (evaluate.py:646-663)",
+        "dense_sdpa_backend": sdpa_name,
+        "dense_ms": round(med["dense"], 1),
+        "fp_v1_ms": round(med["fp_v1"], 1),
+        "mean_native_ms": round(med["mean_native"], 1),
+        "dense_hip_ms": round(med["dense_hip"], 1),
+        "speedup": round(med["dense"] / med["mean_native"], 3),
+        "speedup_vs_dense_hip": round(med["dense_hip"] / med["mean_native"], 3),
+        "all_ms": {label: [round(x, 1) for x in v] for label, v in times.items()},
+        "first_token_ids": tokens,
+        "model_build_s": round(build_s, 1),
+    }
+    del model
+    torch.cuda.empty_cache()
+    return result
+
+
 def cpu_baseline(q, k, v, scale, method, alpha, sample_tiles, budget_s):
     """Time the CPU oracle (reference semantics in numpy float32) on the full
     routing stages plus a sample of query tiles of the attention stages; scale
@@ -295,8 +346,16 @@ def main():
     import torch
     from exp3_amd import _lib, attention, synthetic
 
+    from measure import sweeps
+
     _lib.load()
     device = torch.device("cuda:0")
+    # the reference pins torch SDPA to FLASH_ATTENTION around every prefill
+    # (evaluate.py:630); the same pin (or, if that backend refuses the GQA call
+    # on this GPU, the first accepting one) wraps every timing below
+    sdpa_probe = sweeps.probe_sdpa_backends()
+    sdpa_context, sdpa_name = sweeps.dense_sdpa_context(sdpa_probe)
+    sdpa_context.__enter__()
     scale = 128 ** -0.5
     q, k, v, _ = synthetic.make_inputs(args.seq, seed=args.seed)
     qg, kg, vg = q.to(device), k.to(device), v.to(device)
@@ -325,7 +384,10 @@ def main():
     stages = stage_profile(backend, qg, kg, vg, scale, torch)
     kv_bytes = 2 * args.seq * k.shape[2] * head_dim * 2
     blocks = math.ceil(args.seq / 128)
-    pool_bytes = kv_bytes + kv_bytes // 2 + blocks * k.shape[2] * head_dim * (2 + 4 * 3)
+    # pool: K and V read once; key and value tiles written (padded to whole blocks);
+    # bf16 mean K plus fp32 mean K / mean V / var K descriptors
+    tile_bytes = 2 * blocks * 128 * k.shape[2] * head_dim * 2
+    pool_bytes = kv_bytes + tile_bytes + blocks * k.shape[2] * head_dim * (2 + 4 * 3)
     route_bytes = args.seq * q.shape[2] * head_dim * 2 + blocks * blocks * q.shape[2] * (8 + 1)
     stage_report = {
         "pool": {"ms": round(stages["descriptor"], 4),
@@ -354,6 +416,13 @@ def main():
                                 "block_density": 1.0}
 
     achievable = achievable_peaks(torch)
+    sdpa_context.__exit__(None, None, None)
+
+    full_model = None
+    if not args.no_full_model:
+        full_model = full_model_prefill(args.seq, args.alpha, args.seed, args.model_repeats,
+                                        sdpa_probe, torch)
+        full_model["sdpa_probe"] = sdpa_probe
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -367,7 +436,7 @@ def main():
                 for name in attention.METHODS}
 
     line = {
-        "metric": "sparse-prefill attn ms/layer @32K Qwen2.5-7B shape",
+        "metric": "sparse-prefill attn ms/layer @32K Qwen2.5-7B shape; full-model prefill ms",
         "value": round(ms, 4),
         "unit": "ms",
         "n_gpus": 1,
@@ -407,6 +476,8 @@ def main():
         "block_density": round(density, 5),
         "stages": stage_report,
         "methods": methods,
+        "dense_sdpa_backend": sdpa_name,
+        "full_model": full_model,
         "cpu_baseline": baseline,
     }
     print(json.dumps(line), flush=True)

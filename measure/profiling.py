@@ -92,11 +92,17 @@ def run_attention(args) -> None:
     class Layer:
         layer_idx = 0
 
-    for _ in range(args.repeats):
-        backend.forward(Layer(), q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), None,
-                        args.head_dim ** -0.5)
+    # the reference's SDPA backend pin (evaluate.py:630), as bench.py applies it
+    from measure.sweeps import dense_sdpa_context, probe_sdpa_backends
+    context, sdpa_name = dense_sdpa_context(
+        probe_sdpa_backends(args.head_dim, args.q_heads, args.kv_heads))
+    with context:
+        for _ in range(args.repeats):
+            backend.forward(Layer(), q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                            None, args.head_dim ** -0.5)
     torch.cuda.synchronize()
-    print(f"attention {args.method} S={args.seq} x{args.repeats} done", flush=True)
+    print(f"attention {args.method} S={args.seq} x{args.repeats} done (SDPA pinned to "
+          f"{sdpa_name})", flush=True)
 
 
 def run_copy(args) -> None:

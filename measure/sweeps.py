@@ -145,53 +145,144 @@ def qwen2_7b_config(layers):
                        attn_implementation="sdpa", torch_dtype="bfloat16")
 
 
-def run_model(seq, layers, repeats, seed, methods, alpha, decode_tokens, split_last=False):
+SDPA_ORDER = ("FLASH_ATTENTION", "EFFICIENT_ATTENTION", "MATH")
+
+
+def probe_sdpa_backends(head_dim=128, q_heads=28, kv_heads=4):
+    """Which torch SDPA backends accept the reference's dense prefill call
+    (attention.py:179-189: causal, ``enable_gqa=True``, bf16) on this GPU, each
+    tried alone under ``sdpa_kernel``: name -> "ok" or the error's first line."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    q = torch.randn(1, q_heads, 256, head_dim, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn(1, kv_heads, 256, head_dim, device="cuda", dtype=torch.bfloat16)
+    result = {}
+    for name in SDPA_ORDER:
+        try:
+            with sdpa_kernel(getattr(SDPBackend, name)):
+                F.scaled_dot_product_attention(q, k, k, is_causal=True, scale=head_dim ** -0.5,
+                                               enable_gqa=True)
+            torch.cuda.synchronize()
+            result[name] = "ok"
+        except RuntimeError as exc:
+            result[name] = str(exc).strip().splitlines()[0][:160]
+    return result
+
+
+def dense_sdpa_context(probe):
+    """The reference's contract is ``sdpa_kernel(SDPBackend.FLASH_ATTENTION)``
+    around every prefill (evaluate.py:630); when that backend refuses the GQA call
+    on this GPU, the first accepting backend in torch's priority order is pinned
+    instead. Returns (context manager, backend name)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    for name in SDPA_ORDER:
+        if probe.get(name) == "ok":
+            return sdpa_kernel(getattr(SDPBackend, name)), name
+    raise RuntimeError(f"no SDPA backend accepts the dense GQA call: {probe}")
+
+
+def build_qwen2_7b(layers=28, seed=17):
+    """Random-init Qwen2.5-7B architecture in bf16 on the GPU (no checkpoint)."""
     import torch
     from transformers import Qwen2ForCausalLM
-    from exp3_amd import _lib, attention
-    _lib.load()
-    backend = attention.AttentionBackend(alpha=alpha)   # registers as transformers' "sdpa"
     cfg = qwen2_7b_config(layers)
     torch.manual_seed(seed)
     torch.set_default_dtype(torch.bfloat16)
-    with torch.device("cuda"):
-        model = Qwen2ForCausalLM(cfg)
-    torch.set_default_dtype(torch.float32)
+    try:
+        with torch.device("cuda"):
+            model = Qwen2ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(torch.float32)
     model.eval()
-    params = sum(p.numel() for p in model.parameters())
+    return model
+
+
+def prompt_ids(seq, seed=17, vocab=152064):
+    import torch
     gen = torch.Generator().manual_seed(seed)
-    ids = torch.randint(0, cfg.vocab_size, (1, seq), generator=gen).to("cuda")
+    return torch.randint(0, vocab, (1, seq), generator=gen).to("cuda")
+
+
+def time_prefills(model, backend, ids, cases, repeats, alpha, context):
+    """evaluate.py:323-345 and 630-663: every case warmed up once, then ``repeats``
+    rounds in rotated case order, each prefill timed from a synchronised start
+    through ``model(ids, use_cache=True, logits_to_keep=1)`` and the argmax to a
+    synchronised end, all inside ``context`` (the SDPA backend pin) and inference
+    mode. ``cases``: (label, method, dense_impl). Returns label -> list of ms and
+    label -> first greedy id."""
+    import torch
+
+    def prefill(method, dense_impl):
+        backend.configure(method, alpha)
+        backend.dense_impl = dense_impl
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = model(input_ids=ids, use_cache=True, logits_to_keep=1)
+        token = out.logits[:, -1].argmax(dim=-1)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1000.0
+        del out
+        return ms, int(token.item())
+
+    times = {label: [] for label, _, _ in cases}
+    tokens = {}
+    with torch.inference_mode(), context:
+        for label, method, impl in cases:           # warm-up (evaluate.py:634-644)
+            _, tokens[label] = prefill(method, impl)
+        for r in range(repeats):                     # rotated order (evaluate.py:646-663)
+            order = cases[r % len(cases):] + cases[:r % len(cases)]
+            for label, method, impl in order:
+                ms, _ = prefill(method, impl)
+                times[label].append(ms)
+    return times, tokens
+
+
+def median(values):
+    v = sorted(values)
+    return v[len(v) // 2]
+
+
+def run_model(seq, layers, repeats, seed, methods, alpha, decode_tokens, split_last=False):
+    import torch
+    from exp3_amd import _lib, attention
+    _lib.load()
+    backend = attention.AttentionBackend(alpha=alpha)   # registers as transformers' "sdpa"
+    probe = probe_sdpa_backends()
+    context, sdpa_name = dense_sdpa_context(probe)
+    print(json.dumps({"sweep": "model-sdpa", "probe": probe, "dense_backend": sdpa_name}),
+          flush=True)
+    model = build_qwen2_7b(layers, seed)
+    params = sum(p.numel() for p in model.parameters())
+    ids = prompt_ids(seq, seed, model.config.vocab_size)
+    cases = [(m, m, "sdpa") for m in methods]
+    if "dense" in methods:
+        cases.append(("dense_hip", "dense", "hip"))
+    times, tokens = time_prefills(model, backend, ids, cases, repeats, alpha, context)
+    dense_ms = median(times["dense"]) if "dense" in times else None
+    for label, method, impl in cases:
+        med = median(times[label])
+        print(json.dumps({"sweep": "model", "method": label,
+                          "alpha": alpha if method != "dense" else None,
+                          "dense_backend": (sdpa_name if impl == "sdpa" else "hip attn_kernel")
+                          if method == "dense" else None,
+                          "seq": seq, "layers": layers, "params": params,
+                          "prefill_ms_median": round(med, 1),
+                          "prefill_ms_all": [round(x, 1) for x in times[label]],
+                          "first_token_id": tokens[label],
+                          "speedup_vs_dense": round(dense_ms / med, 3) if dense_ms else None}),
+              flush=True)
+    backend.dense_impl = "sdpa"
 
     def prefill(method):
         backend.configure(method, alpha)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
         with torch.no_grad():
             out = model(ids, use_cache=True, logits_to_keep=1)
-            token = out.logits[:, -1].argmax(-1)
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) * 1000.0, out, token
+        return out, out.logits[:, -1].argmax(-1)
 
-    for m in methods:                        # warm-up, one prefill per method
-        prefill(m)
-    times = {m: [] for m in methods}
-    for r in range(repeats):                 # rotated method order
-        order = methods[r % len(methods):] + methods[:r % len(methods)]
-        for m in order:
-            ms, _, _ = prefill(m)
-            times[m].append(ms)
-    dense_ms = sorted(times["dense"])[len(times["dense"]) // 2] if "dense" in times else None
-    for m in methods:
-        med = sorted(times[m])[len(times[m]) // 2]
-        print(json.dumps({"sweep": "model", "method": m, "alpha": alpha if m != "dense" else None,
-                          "seq": seq, "layers": layers, "params": params,
-                          "prefill_ms_median": round(med, 1),
-                          "prefill_ms_all": [round(x, 1) for x in times[m]],
-                          "speedup_vs_dense": round(dense_ms / med, 3) if dense_ms else None}),
-              flush=True)
     if split_last:   # evaluate.py:357-380, split_last_prompt_token=True (not timed)
         for m in methods:
-            _, _, full_token = prefill(m)
+            _, full_token = prefill(m)
             with torch.no_grad():
                 pre = model.model(input_ids=ids[:, :-1], use_cache=True)
                 step = model(input_ids=ids[:, -1:], past_key_values=pre.past_key_values,
@@ -203,7 +294,7 @@ def run_model(seq, layers, repeats, seed, methods, alpha, decode_tokens, split_l
                               "full_prefill_id": int(full_token.item()),
                               "split_id": int(split_token.item())}), flush=True)
     # greedy dense decode (not timed): exercises the backend's decode branch
-    _, out, token = prefill("dense")
+    out, token = prefill("dense")
     cache = out.past_key_values
     generated = [int(token.item())]
     with torch.no_grad():
