@@ -26,6 +26,8 @@
 //     plus one lane-half exchange; the second pass recomputes the logits, and the
 //     per-block sum over the tile's rows is a 16-shuffle transpose-reduction across
 //     lanes plus a fixed-order add of the four waves' partial sums.
+#include <mutex>
+
 #include "common.h"
 
 namespace spx {
@@ -346,11 +348,13 @@ extern "C" int64_t spx_selector_workspace_bytes(int batch, int seq, int kv_heads
   return (int64_t)batch * kv_heads * selector_chunks(seq) * kSelChunkElems * 2;
 }
 
-extern "C" int spx_selector_scores(const void* q, const int64_t* q_strides, const float* mean_k,
-                                   const float* var_k, const float* sigma_v, const int32_t* counts,
-                                   int batch, int seq, int q_heads, int kv_heads, int head_dim,
-                                   int block_size, int selector, float scale, void* workspace,
-                                   float* score, const int64_t* score_strides, void* stream) {
+namespace {
+
+int run_selectors(const void* q, const int64_t* q_strides, const float* mean_k,
+                  const float* var_k, const float* sigma_v, const int32_t* counts, int batch,
+                  int seq, int q_heads, int kv_heads, int head_dim, int block_size, int selector,
+                  float scale, void* workspace, float* score, const int64_t* score_strides,
+                  void* stream) {
   SPX_REQUIRE(selector == SPX_SELECTOR_MEAN_BALANCED || selector == SPX_SELECTOR_CGF_MEAN ||
                   selector == SPX_SELECTOR_DISPERSION_MEAN,
               SPX_EINVAL, "unsupported selector id %d", selector);
@@ -407,4 +411,88 @@ extern "C" int spx_selector_scores(const void* q, const int64_t* q_strides, cons
       break;
   }
   return launch_status("selector_scores");
+}
+
+}  // namespace
+
+extern "C" int spx_selector_scores(const void* q, const int64_t* q_strides, const float* mean_k,
+                                   const float* var_k, const float* sigma_v, const int32_t* counts,
+                                   int batch, int seq, int q_heads, int kv_heads, int head_dim,
+                                   int block_size, int selector, float scale, void* workspace,
+                                   float* score, const int64_t* score_strides, void* stream) {
+  return run_selectors(q, q_strides, mean_k, var_k, sigma_v, counts, batch, seq, q_heads,
+                       kv_heads, head_dim, block_size, selector, scale, workspace, score,
+                       score_strides, stream);
+}
+
+// ------------------------------------------------ no-allocation variant
+//
+// The split workspace of spx_selector_scores_noalloc lives in a file-scope device
+// array, so the entry point needs no caller workspace and allocates nothing
+// (callers under graph capture, tight serving loops). Every GPU holds its own copy
+// of the array until the process ends; its device address is looked up once per
+// device with hipGetSymbolAddress (the array's name in host code is only a
+// host-side stand-in and must never reach a kernel). The split kernel rewrites
+// every workspace entry a call reads (padded block rows as zeros), so nothing is
+// cleared between calls; calls that overlap on one GPU race on the array.
+
+constexpr int64_t kSelectorScratchBytes = 8ll << 20;   // B * Hkv * ceil(NB / 32) <= 256
+
+static __device__ __align__(256) uint8_t scratch[kSelectorScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on first use).
+int scratch_address(void* stream, void** out) {
+  int device = -1;
+  hipError_t e = hipGetDevice(&device);
+  SPX_REQUIRE(e == hipSuccess, SPX_ELAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  SPX_REQUIRE(device >= 0 && device < kMaxDevices, SPX_EUNSUPPORTED,
+              "device %d beyond the %d devices the scratch table covers", device, kMaxDevices);
+  if (stream != nullptr) {
+    int stream_device = -1;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &stream_device);
+    SPX_REQUIRE(e == hipSuccess, SPX_EINVAL, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+    SPX_REQUIRE(stream_device == device, SPX_EINVAL,
+                "stream belongs to device %d but device %d is current", stream_device, device);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[device] == nullptr) {
+    void* address = nullptr;
+    e = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    SPX_REQUIRE(e == hipSuccess && address != nullptr, SPX_ELAUNCH,
+                "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                hipGetErrorString(e));
+    g_scratch[device] = address;
+  }
+  *out = g_scratch[device];
+  return SPX_OK;
+}
+
+}  // namespace
+
+extern "C" int spx_selector_scores_noalloc(const void* q, const int64_t* q_strides,
+                                           const float* mean_k, const float* var_k,
+                                           const float* sigma_v, const int32_t* counts, int batch,
+                                           int seq, int q_heads, int kv_heads, int head_dim,
+                                           int block_size, int selector, float scale, float* score,
+                                           const int64_t* score_strides, void* stream) {
+  const int64_t need = spx_selector_workspace_bytes(batch, seq, kv_heads, head_dim);
+  SPX_REQUIRE(need > 0, SPX_EUNSUPPORTED,
+              "bad or unsupported shape: batch %d seq %d kv_heads %d head_dim %d", batch, seq,
+              kv_heads, head_dim);
+  SPX_REQUIRE(need <= kSelectorScratchBytes, SPX_EUNSUPPORTED,
+              "workspace of %lld bytes exceeds the %lld-byte static scratch (batch x kv_heads x "
+              "ceil(blocks / 32) must be at most 256); use spx_selector_scores with a caller "
+              "workspace", (long long)need, (long long)kSelectorScratchBytes);
+  void* workspace = nullptr;
+  const int rc = scratch_address(stream, &workspace);
+  if (rc) return rc;
+  return run_selectors(q, q_strides, mean_k, var_k, sigma_v, counts, batch, seq, q_heads,
+                       kv_heads, head_dim, block_size, selector, scale, workspace, score,
+                       score_strides, stream);
 }

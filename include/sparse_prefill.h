@@ -40,7 +40,7 @@ extern "C" {
 #define SPX_EUNSUPPORTED (-2) /* valid in the reference, not built here       */
 #define SPX_ELAUNCH (-3)      /* HIP launch / runtime failure                 */
 
-#define SPX_ABI_VERSION 5
+#define SPX_ABI_VERSION 6
 
 /* Selector ids for spx_selector_scores (kernels.py:62). */
 #define SPX_SELECTOR_MEAN_BALANCED 0
@@ -159,6 +159,21 @@ int spx_selector_scores(const void* q, const int64_t* q_strides, const float* me
 /* Bytes of the spx_selector_scores workspace (B * Hkv * ceil(NB / 32) * 32 KB), or -1
  * for an unsupported shape. Helper of spx_selector_scores (no reference counterpart). */
 int64_t spx_selector_workspace_bytes(int batch, int seq, int kv_heads, int head_dim);
+
+/* spx_selector_scores without the workspace argument and without any allocation: the
+ * split workspace is a file-scope device array of 8 MiB per GPU (held until the
+ * process ends), so the shape must satisfy B * Hkv * ceil(NB / 32) <= 256, i.e.
+ * spx_selector_workspace_bytes() <= 8 MiB (larger shapes return SPX_EUNSUPPORTED).
+ * Results are identical to spx_selector_scores'. The stream must belong to the
+ * current device. Calls that overlap on one GPU race on the shared array.
+ * No counterpart in the reference: an entry point for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops). */
+int spx_selector_scores_noalloc(const void* q, const int64_t* q_strides, const float* mean_k,
+                                const float* var_k, const float* sigma_v,
+                                const int32_t* counts, int batch, int seq, int q_heads,
+                                int kv_heads, int head_dim, int block_size, int selector,
+                                float scale, float* score, const int64_t* score_strides,
+                                void* stream);
 
 /* ----------------------------------------------------------- attention */
 
