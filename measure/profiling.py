@@ -5,6 +5,8 @@ Workloads (run as the program after ``rocprofv3 ... --``):
   python -m measure.profiling attention [--seq 32640] [--method mean_native] [--repeats 2]
                                          [--q-heads 28 --kv-heads 4 --head-dim 128] [--dense-impl sdpa]
       one prefill attention layer (pool, route, attention) per repeat, as bench.py runs it
+  python -m measure.profiling gemm [--n 16384] [--repeats 3]
+      the hipBLASLt bf16 GEMM bench.py reports as the achievable MFMA ceiling
   python -m measure.profiling copy [--gib 1]
       a plain device copy of known size (torch copy_), the calibration for the
       FETCH_SIZE / WRITE_SIZE counters
@@ -105,6 +107,19 @@ def run_attention(args) -> None:
           f"{sdpa_name})", flush=True)
 
 
+def run_gemm(args) -> None:
+    """The achievable-peak reference bench.py times: a bf16 GEMM (hipBLASLt through
+    torch.matmul) on N(0,1) operands, ``repeats`` times."""
+    import torch
+    n = args.n
+    a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    for _ in range(args.repeats):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    print(f"gemm {n}^3 x{args.repeats} done", flush=True)
+
+
 def run_copy(args) -> None:
     import torch
     n = int(args.gib * (1 << 30)) // 2
@@ -129,6 +144,9 @@ def main(argv=None) -> int:
     a.add_argument("--kv-heads", type=int, default=4)
     a.add_argument("--head-dim", type=int, default=128)
     a.add_argument("--dense-impl", default="sdpa", choices=("sdpa", "hip"))
+    g = sub.add_parser("gemm")
+    g.add_argument("--n", type=int, default=16384)
+    g.add_argument("--repeats", type=int, default=3)
     c = sub.add_parser("copy")
     c.add_argument("--gib", type=float, default=1.0)
     c.add_argument("--repeats", type=int, default=3)
@@ -147,6 +165,8 @@ def main(argv=None) -> int:
         run_attention(args)
     elif args.cmd == "copy":
         run_copy(args)
+    elif args.cmd == "gemm":
+        run_gemm(args)
     else:
         print(json.dumps(traffic(args), indent=2))
     return 0
