@@ -42,7 +42,11 @@ HIPCC_FLAGS = [
 # and copies all 128 registers in and out every iteration (8 extra instructions per
 # MFMA). The VGPR form keeps O where it is accumulated: 12.1 -> 8.2 ms per
 # 32640-token layer.
-EXTRA_FLAGS = {"attn256.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# route.hip: the V1 score reduction reads every MFMA result with VALU instructions;
+# in the VGPR form they read the accumulators in place instead of copying them out
+# of AGPRs first (16 copies per 32-block chunk and wave).
+EXTRA_FLAGS = {"attn256.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "route.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def _hipcc() -> str:

@@ -9,11 +9,11 @@
 //     S[row][j] = q_row . Kbar_j          (v_mfma_f32_32x32x16_bf16, fp32 acc)
 //     x = S * fp32(scale * log2 e)
 // Row i of tile t is valid for block j iff i >= 128 (j + 1) - 1 and i < S. Each
-// lane reduces its 16 rows of one block column to (max, sum 2^(x - max)) and
-// merges with the other lane half; the four waves' partials of a chunk are merged
-// in a fixed order after the next chunk's barrier, giving M_tj and m_tj. The
-// normalisation w_j = m_tj 2^(M_tj - max_j M_tj) / (sum_j w + 1e-9) runs in the
-// same workgroup, so the raw scores never reach HBM.
+// lane reduces its 16 rows of one block column to (max, sum 2^(x - max)); the
+// eight partials of a chunk (4 waves x 2 lane halves) are merged in a fixed order
+// after the next chunk's barrier, giving M_tj and m_tj. One wave then runs the
+// normalisation w_j = m_tj 2^(M_tj - max_j M_tj) / (sum_j w + 1e-9) and the
+// selection of the row, so the raw scores never reach HBM.
 //
 // Selection (upstream :357-407 and kernels.py:129-160) is one shared device
 // routine over a score row held in LDS: threshold fp32(max * alpha), protected
@@ -131,6 +131,40 @@ __device__ void select_row(const float* row, int t, const SelectParams& p, const
       o.indices[o.row_base + (int64_t)pos * o.heads] = kb;
   }
   if (o.counts && tid == 0) o.counts[o.count_off] = base;
+}
+
+// V1 selection (upstream :357-407 with min_budget = 0) of one score row in LDS, by
+// one wave: the same rule as select_row, compacted 64 key blocks per ballot.
+__device__ void select_v1_row_wave(const float* row, int t, const SelectParams& p,
+                                   const SelectOut& o) {
+  const int lane = threadIdx.x & 63;
+  const int kb = p.key_blocks;
+  float local = -INFINITY;
+  for (int j = lane; j < kb; j += 64) local = max_nan(local, row[j]);
+  const float maximum = wave_max(local);
+  const float threshold = maximum * p.alpha;   // fp32(max * fp32(alpha))
+  const bool last_rows = t >= p.query_blocks - p.last;
+  int base = 0;
+  for (int j0 = 0; j0 < kb; j0 += 64) {
+    const int j = j0 + lane;
+    bool active = false;
+    if (j < kb) {
+      const bool keep = row[j] >= threshold;
+      const int distance = t - j;
+      const bool prot = j < p.sink || (distance >= 0 && distance < p.window) || last_rows;
+      active = (keep || prot) && distance >= 0;
+      if (o.mask) o.mask[o.row_base + (int64_t)j * o.heads] = active ? 1 : 0;
+    }
+    const uint64_t ballot = __ballot(active);
+    const int before = __popcll(ballot & ((1ull << lane) - 1ull));
+    if (active && o.indices) o.indices[o.row_base + (int64_t)(base + before) * o.heads] = j;
+    base += __popcll(ballot);
+  }
+  if (o.indices) {
+    for (int pos = base + lane; pos < kb; pos += 64)
+      o.indices[o.row_base + (int64_t)pos * o.heads] = kb;
+  }
+  if (o.counts && lane == 0) o.counts[o.count_off] = base;
 }
 
 // ------------------------------------------------------------ V1 scores
@@ -254,10 +288,8 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   const int col = lane & 31, half = lane >> 5;
 
   __shared__ __align__(16) uint16_t ring[R][Ring::kSlotElems];
-  __shared__ float part_max[2][4][32];   // per-wave (max, mass) of the last two chunks
-  __shared__ float part_mass[2][4][32];
-  __shared__ float scratch[8];
-  __shared__ int wave_counts[8];
+  __shared__ float part_max[2][8][32];   // per lane half (max, mass) of the last two chunks
+  __shared__ float part_mass[2][8][32];
   extern __shared__ float v1_lds[];
   const int nb = a.blocks;
   float* blk_max = v1_lds;
@@ -321,32 +353,22 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
       chunk_column<kPosScale, true>(acc, c, kBlock * (j - t) + kBlock - 1, rows_left, wave,
                                     lane, mx, mass);
     }
-    // merge the two lane halves (rows 4*half + ...)
-    {
-      const float om = xor32(mx), os = xor32(mass);
-      const float nm = fmaxf(mx, om);
-      float merged = 0.0f;
-      if (nm != -INFINITY) {
-        merged = (mx == -INFINITY ? 0.0f : mass * exp2_fast(mx - nm)) +
-                 (om == -INFINITY ? 0.0f : os * exp2_fast(om - nm));
-      }
-      mx = nm;
-      mass = merged;
-    }
-    if (half == 0) {
-      part_max[jc & 1][wave][col] = mx;
-      part_mass[jc & 1][wave][col] = mass;
-    }
+    // every lane half's partial (16 rows) goes to LDS; merge_chunk combines them
+    part_max[jc & 1][2 * wave + half][col] = mx;
+    part_mass[jc & 1][2 * wave + half][col] = mass;
   };
-  // the four waves' partials of chunk jc -> blk_max / blk_mass (threads 0..31)
+  // the eight partials (4 waves x 2 lane halves) of chunk jc -> blk_max / blk_mass,
+  // in a fixed order (threads 0..31)
   auto merge_chunk = [&](int jc) {
     const int jj = jc * 32 + tid;
     if (tid < 32 && jj < nb) {
       float m = part_max[jc & 1][0][tid];
-      for (int w = 1; w < 4; ++w) m = fmaxf(m, part_max[jc & 1][w][tid]);
+#pragma unroll
+      for (int w = 1; w < 8; ++w) m = fmaxf(m, part_max[jc & 1][w][tid]);
       float s2 = 0.0f;
       if (m != -INFINITY) {
-        for (int w = 0; w < 4; ++w) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
           const float pm = part_max[jc & 1][w][tid];
           if (pm != -INFINITY) s2 += part_mass[jc & 1][w][tid] * exp2_fast(pm - m);
         }
@@ -374,26 +396,29 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   block_sync();
   if (nchunks > 0) merge_chunk(nchunks - 1);
   block_sync();
+  // One wave finishes the row: normalisation and selection touch at most NB
+  // (<= 1024) entries, 16 per lane, and in one wave they need no barriers or
+  // cross-wave reductions; the other waves end here.
+  if (wave != 0) return;
 
   // normalize_scores over j <= t; j > t has M = -inf and contributes 0.
   float local = -INFINITY;
-  for (int jj = tid; jj <= t; jj += kRouteThreads) local = fmaxf(local, blk_max[jj]);
-  const float gmax = block_reduce_max(local, scratch);
+  for (int jj = lane; jj <= t; jj += 64) local = fmaxf(local, blk_max[jj]);
+  const float gmax = wave_max(local);
   float wsum = 0.0f;
-  for (int jj = tid; jj <= t; jj += kRouteThreads) {
+  for (int jj = lane; jj <= t; jj += 64) {
     const float m = blk_max[jj];
     const float w = (m != -INFINITY) ? blk_mass[jj] * exp2_fast(m - gmax) : 0.0f;
     blk_mass[jj] = w;
     wsum += w;
   }
-  const float total = block_reduce_sum(wsum, scratch) + 1e-9f;
-  for (int jj = tid; jj < a.blocks; jj += kRouteThreads) {
+  const float total = wave_sum(wsum) + 1e-9f;
+  for (int jj = lane; jj < a.blocks; jj += 64) {
     const float s = jj <= t ? blk_mass[jj] / total : 0.0f;
     blk_mass[jj] = s;
     if (a.score) a.score[b * a.ss_b + t * a.ss_t + jj * a.ss_j + h * a.ss_h] = s;
   }
   if (a.indices) {
-    block_sync();
     SelectOut o;
     o.indices = a.indices;
     o.counts = a.counts;
@@ -401,7 +426,7 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
     o.heads = a.q_heads;
     o.row_base = (((int64_t)b * a.blocks + t) * a.blocks) * a.q_heads + h;
     o.count_off = ((int64_t)b * a.blocks + t) * a.q_heads + h;
-    select_row(blk_mass, t, a.sel, o, scratch, wave_counts);
+    select_v1_row_wave(blk_mass, t, a.sel, o);
   }
 }
 
