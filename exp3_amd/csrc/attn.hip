@@ -6,7 +6,8 @@
 // index list in order; every listed 128-key block j contributes all its keys
 // (keys past the sequence end read as zero), causality is applied only inside the
 // block j == t; O = softmax(scale q K^T) V is stored as bf16 and the natural-log
-// LSE = M ln 2 + ln l. List entries outside [0, NB) are skipped. With the mean
+// LSE = M ln 2 + ln l. List entries outside [0, NB) are skipped; a block listed
+// n times is attended n times, as the reference's list walk does. With the mean
 // correction, each row also attends to the fp32 block-mean key of every block
 // j < t missing from its list (logit + ln n_j) with the block-mean value, inside
 // the same online softmax; this equals the logaddexp merge of kernels.py:179-230
@@ -17,7 +18,7 @@
 //     waves 0-3 own the 128 rows of tile t, waves 4-7 those of tile t - 1, 32 rows
 //     each. The two tiles' block lists are merged, so every K/V tile copied into
 //     LDS serves both (the lists differ by little: sinks, window and most routed
-//     blocks are shared).
+//     blocks are shared); a block repeated in a list is repeated in the merged one.
 //   * Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16:
 //     each lane owns one query column, so row max / row sum are in-lane reductions
 //     plus one exchange with the other lane half, the O rescale is a per-lane
@@ -598,9 +599,12 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
 
   __shared__ __align__(16) uint16_t kbuf[2][kBlock * kBlock];
   __shared__ __align__(16) uint16_t vbuf[2][kBlock * kBlock];
-  __shared__ int16_t ulist[kMaxBlocksAttn];          // union of both lists, ascending
-  __shared__ uint8_t uflag[kMaxBlocksAttn];          // bit i: block listed for item i
-  __shared__ uint32_t bits[2][kMaxBlocksAttn / 32];  // per-item membership
+  // union of both lists, ascending; a block listed n times for an item appears
+  // max over the items of n times, occurrence k flagged for the items listing it
+  // more than k times (the reference attends a repeated list entry repeatedly)
+  __shared__ int16_t ulist[2 * kMaxBlocksAttn];
+  __shared__ uint8_t uflag[2 * kMaxBlocksAttn];      // bit i: occurrence is item i's
+  __shared__ uint32_t mult[2][kMaxBlocksAttn / 2];   // per-item times listed, 16 bits per block
   __shared__ float tail_bias[2][kTailTile];
   __shared__ int wave_counts[kAttnThreads / 64];
 
@@ -638,8 +642,8 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
     for (int db = 0; db < 4; ++db) ws.o[db] = f32x16{};
   }
 
-  // ---- membership bitmaps of both items' lists (valid ids), then their union
-  if (tid < 2 * (kMaxBlocksAttn / 32)) (&bits[0][0])[tid] = 0u;
+  // ---- how often each block is listed for each item (valid ids), then the union
+  for (int x = tid; x < kMaxBlocksAttn; x += kAttnThreads) (&mult[0][0])[x] = 0u;
   block_sync();
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
@@ -651,33 +655,42 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
       const int64_t* list = a.idx + b * a.is_b + tt * a.is_t + h * a.is_h;
       for (int pos = tid; pos < count; pos += kAttnThreads) {
         const int j = (int)list[pos * a.is_p];
-        if (j >= 0 && j < a.blocks) atomicOr(&bits[it][j >> 5], 1u << (j & 31));
+        if (j >= 0 && j < a.blocks) atomicAdd(&mult[it][j >> 1], 1u << ((j & 1) * 16));
       }
     } else {
-      for (int j = tid; j <= tt; j += kAttnThreads) atomicOr(&bits[it][j >> 5], 1u << (j & 31));
+      for (int j = tid; j <= tt; j += kAttnThreads) atomicAdd(&mult[it][j >> 1], 1u << ((j & 1) * 16));
     }
   }
   block_sync();
   // Processing order: every listed block except the two diagonal ones (t, t - 1),
   // ascending, then the diagonal ones. The block loop for the first part has a
   // single (unmasked) code path, which keeps O in one register set.
+  auto times_listed = [&](int it, int j) {
+    return (int)((mult[it][j >> 1] >> ((j & 1) * 16)) & 0xffffu);
+  };
   int nu = 0;
   auto compact = [&](bool diagonal_pass) {
     for (int j0 = 0; j0 < a.blocks; j0 += kAttnThreads) {
       const int j = j0 + tid;
-      int f = 0;
-      if (j < a.blocks && ((j == t_item[0] || j == t_item[1]) == diagonal_pass))
-        f = ((bits[0][j >> 5] >> (j & 31)) & 1u) | (((bits[1][j >> 5] >> (j & 31)) & 1u) << 1);
-      const bool flag = f != 0;
-      const uint64_t ballot = __ballot(flag);
-      const int before = __popcll(ballot & ((1ull << lane) - 1ull));
-      if (lane == 0) wave_counts[w] = __popcll(ballot);
+      int c0 = 0, c1 = 0;
+      if (j < a.blocks && ((j == t_item[0] || j == t_item[1]) == diagonal_pass)) {
+        c0 = times_listed(0, j);
+        c1 = times_listed(1, j);
+      }
+      const int e = max(c0, c1);   // occurrences of block j in the union
+      int incl = e;                // inclusive prefix sum over the wave
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d);
+        if (lane >= d) incl += v;
+      }
+      if (lane == 63) wave_counts[w] = incl;
       block_sync();
-      int offset = nu;
+      int offset = nu + incl - e;
       for (int x = 0; x < w; ++x) offset += wave_counts[x];
-      if (flag) {
-        ulist[offset + before] = (int16_t)j;
-        uflag[offset + before] = (uint8_t)f;
+      for (int k = 0; k < e; ++k) {
+        ulist[offset + k] = (int16_t)j;
+        uflag[offset + k] = (uint8_t)((c0 > k ? 1 : 0) | (c1 > k ? 2 : 0));
       }
       for (int x = 0; x < kAttnThreads / 64; ++x) nu += wave_counts[x];
       block_sync();
@@ -774,7 +787,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
       const int tt = t_item[it];
       for (int j0 = 0; j0 < max(tt, 0); j0 += kAttnThreads) {
         const int j = j0 + tid;
-        const bool in_tail = j < tt && ((bits[it][j >> 5] >> (j & 31)) & 1u) == 0u;
+        const bool in_tail = j < tt && times_listed(it, j) == 0;
         const uint64_t ballot = __ballot(in_tail);
         const int before = __popcll(ballot & ((1ull << lane) - 1ull));
         if (lane == 0) wave_counts[w] = __popcll(ballot);

@@ -284,6 +284,55 @@ def test_exact_attention_edge_lists(gpu):
     assert (a_out[~finite] == 0).all()
 
 
+def test_exact_attention_repeated_list_entries(gpu):
+    """A block listed twice is attended twice, as the reference's list walk does
+    (upstream:305-340) and the oracle restates: its keys enter the softmax with
+    double weight. Lists hold at most NB entries, so repeats go into slots freed by
+    dropped blocks: repeats in the full-block path, on the diagonal, one tile of a
+    pair repeating a block the other lists once, a block listed three times, and a
+    list of one block listed twice."""
+    length = 1089
+    q, k, v = inputs(length, seed=4)
+    qg, kg, vg = _gpu(q, k, v)
+    blocks = ref.num_blocks(length)           # 9
+    sel = np.broadcast_to(np.tril(np.ones((blocks, blocks), bool))[None, :, :, None],
+                          (1, blocks, blocks, 28)).copy()
+    sel[0, 8, [4, 6], 0] = False              # tile 8, head 0: room for 2 repeats
+    sel[0, 8, [4, 6], 2] = False
+    sel[0, 7, 5, 1] = False                   # tile 7, head 1: room for 2
+    idx, cnt = ref.indices_from_mask(sel)
+
+    def append(t, h, *ids):
+        for j in ids:
+            assert cnt[0, t, h] < blocks
+            idx[0, t, cnt[0, t, h], h] = j
+            cnt[0, t, h] += 1
+
+    append(8, 0, 3, 3)        # tile 8 lists block 3 three times; tile 7 lists it once
+    append(7, 1, 0, 0)        # tile 7: block 0 three times
+    append(8, 2, 8, 1)        # the diagonal block twice, block 1 twice
+    append(5, 4, 2, 4, 5)     # repeats of history and window blocks, and the diagonal
+    idx[0, 3, :, 6] = blocks  # tile 3, head 6: only block 1, listed twice
+    idx[0, 3, :2, 6] = 1
+    cnt[0, 3, 6] = 2
+    out, lse = up.exact_attention(qg, kg, vg, torch.from_numpy(idx).cuda(),
+                                  torch.from_numpy(cnt).cuda(), SCALE)
+    e_out, e_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE)
+    assert_output_close(to_np(out), e_out, what="repeated entries")
+    np.testing.assert_allclose(to_np(lse), e_lse, atol=0.02, rtol=0.01)
+    # the repeats matter: the same lists without them give a visibly different answer
+    plain_idx, plain_cnt = ref.indices_from_mask(ref.mask_from_indices(idx, cnt))
+    p_out, p_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), plain_idx, plain_cnt,
+                                       SCALE)
+    for t, h in ((8, 0), (7, 1), (8, 2), (5, 4)):
+        rows = slice(t * 128, (t + 1) * 128)
+        assert np.abs(p_out[0, rows, h] - e_out[0, rows, h]).max() > 0.02, (t, h)
+    # one block listed twice: the same softmax, every weight doubled -> LSE + ln 2
+    rows = slice(3 * 128, 4 * 128)
+    np.testing.assert_allclose(to_np(lse)[0, rows, 6] - p_lse[0, rows, 6], np.log(2.0),
+                               atol=0.02)
+
+
 @pytest.mark.parametrize("length", (257, 1089))
 def test_mean_tail_and_merge(gpu, length):
     q, k, v = inputs(length, seed=37)
