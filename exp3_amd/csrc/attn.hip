@@ -89,6 +89,17 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& v, int base) {
   return as_bf16x8(w);
 }
 
+// The running-max rescale multiplies the O accumulators in place from inline
+// assembly (tied operands keep O in its registers across the rarely taken
+// branch). The compiler's hazard recognizer does not look inside asm statements,
+// so the wait states an MFMA that wrote O needs before VALU access to O are issued
+// here, at the top of that branch: the products into O are issued before the
+// branch (their results are live on both of its paths), so these wait states sit
+// between the last product and the first multiply. 19 >= the 16-pass XDL write ->
+// VALU read / write requirement of the gfx940 family (the 8-pass products here
+// need fewer). Not tied to O: tying it changes how the loop is scheduled.
+__device__ __forceinline__ void o_settle() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 2"); }
+
 // Per-wave online-softmax state for its 32 query columns.
 struct WaveState {
   bf16x8 qb[8];   // Q^T B operands, dim chunk dc
@@ -223,6 +234,7 @@ __device__ __forceinline__ void softmax(f32x16 (&s)[4], WaveState& ws, float sca
     const float corr = (m_new == ws.m) ? 1.0f : exp2_fast(ws.m - m_new);
     // in place (tied operands): O keeps its registers across the rarely taken
     // branch instead of being copied into a second set on every block
+    o_settle();
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
@@ -391,6 +403,7 @@ __device__ __forceinline__ void shift_and_check(f32x16& sv, WaveState& ws, float
     // nothing is accumulated before the first move (thr -inf): O and l stay 0
     const float corr = ws.thr == -INFINITY ? 0.0f : exp2_fast(-d);
     // in place (tied operands): O keeps its registers across the rarely taken branch
+    o_settle();
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll

@@ -202,7 +202,13 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
       const float d = move ? mx : 0.0f;
       // nothing is accumulated before the first move (thr -inf): O and l stay 0
       const float corr = thr == -INFINITY ? 0.0f : exp2_fast(-d);
-      // in place (tied operands): O keeps its registers across the rare branch
+      // in place (tied operands): O keeps its registers across the rare branch. The
+      // compiler's hazard recognizer does not look inside asm statements, so the
+      // wait states after the last product into O (19 >= the XDL write -> VALU
+      // requirement) are issued first, tied to O.
+      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 2"
+                   : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(o[4]), "+v"(o[5]),
+                     "+v"(o[6]), "+v"(o[7]));
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
