@@ -3,6 +3,7 @@ reduction that ``bench.py`` reports as ``roofline.traffic``.
 
 Workloads (run as the program after ``rocprofv3 ... --``):
   python -m measure.profiling attention [--seq 32640] [--method mean_native] [--repeats 2]
+                                        [--qk-scale 4 --alpha 0.7]  (sparse selections)
                                          [--q-heads 28 --kv-heads 4 --head-dim 128] [--dense-impl sdpa]
       one prefill attention layer (pool, route, attention) per repeat, as bench.py runs it
   python -m measure.profiling gemm [--n 16384] [--repeats 3]
@@ -87,6 +88,9 @@ def run_attention(args) -> None:
     _lib.load()
     q, k, v, _ = synthetic.make_inputs(args.seq, seed=args.seed, q_heads=args.q_heads,
                                        kv_heads=args.kv_heads, head_dim=args.head_dim, device="cuda")
+    if args.qk_scale != 1.0:   # sharpened scores: sparse selections (the sparse sweep's inputs)
+        q = (q.float() * args.qk_scale).to(torch.bfloat16)
+        k = (k.float() * args.qk_scale).to(torch.bfloat16)
     backend = attention.AttentionBackend(alpha=args.alpha, register=False,
                                          dense_impl=args.dense_impl)
     backend.configure(args.method, args.alpha)
@@ -144,6 +148,8 @@ def main(argv=None) -> int:
     a.add_argument("--kv-heads", type=int, default=4)
     a.add_argument("--head-dim", type=int, default=128)
     a.add_argument("--dense-impl", default="sdpa", choices=("sdpa", "hip"))
+    a.add_argument("--qk-scale", type=float, default=1.0,
+                   help="multiply Q and K (bf16) to sharpen the routing, as the sparse sweep")
     g = sub.add_parser("gemm")
     g.add_argument("--n", type=int, default=16384)
     g.add_argument("--repeats", type=int, default=3)
