@@ -18,6 +18,10 @@
       check_qwen35_math.py): dense (torch SDPA and the HIP kernel) and fp_v1 at
       alpha 0.08; ms/layer, the attention kernel's HIP-event time and its rate over
       the selected 128 x 128 tiles (4 x 128 x 128 x 256 FLOP each)
+  python -m measure.sweeps pair-overlap [--seq 32640] [--qk-scale 4] [--alpha 0.7]
+      fp_v1 on sharpened inputs: the attention kernel on the routed lists and on
+      lists where each tile pair's lists coincide (tile t - 1 takes tile t's routed
+      blocks), the cost of pairing tiles whose lists differ
   python -m measure.sweeps model [--seq 32640] [--layers 28] [--repeats 3]
       full prefill of a random-init Qwen2.5-7B-shaped model built from a local
       config (28 layers, hidden 3584, FFN 18944, 28/4 heads, RMSNorm 1e-6,
@@ -134,6 +138,63 @@ def run_d256(seq, seed):
         row.update({"sweep": "d256", "q_heads": 16, "kv_heads": 4, "head_dim": 256,
                     "impl": dense_impl if method == "dense" else "hip"})
         print(json.dumps(row), flush=True)
+
+
+def run_pair_overlap(seq, seed, qk_scale, alpha):
+    """fp_v1 on sharpened inputs: the attention kernel's time on the routed lists and
+    on lists where tile t - 1 takes tile t's routed blocks below it (its diagonal
+    added), so that each tile pair's lists coincide; bounds what pairing tiles on
+    list overlap can give."""
+    import numpy as np
+    import torch
+    from exp3_amd import _lib, attention, kernels, synthetic
+    _lib.load()
+    q, k, v, _ = synthetic.make_inputs(seq, seed=seed, device="cuda")
+    q = (q.float() * qk_scale).to(torch.bfloat16)
+    k = (k.float() * qk_scale).to(torch.bfloat16)
+    scale = 128 ** -0.5
+    b = attention.AttentionBackend(alpha=alpha, register=False)
+    b.configure("fp_v1", alpha)
+    _, _, tiles, _, idx, cnt, sel = b._route_v1(q, k, v, scale, {"events": {}}, False, True)
+    blocks = sel.shape[1]
+
+    def timed(i, c, n=10):
+        for _ in range(3):
+            b._attention(q, k, tiles, i, c, scale, None)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            b._attention(q, k, tiles, i, c, scale, None)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    def union_efficiency(m):
+        union = 0
+        for tp in range((blocks + 1) // 2):
+            t1, t2 = blocks - 1 - 2 * tp, blocks - 2 - 2 * tp
+            union += (m[t1] | (m[t2] if t2 >= 0 else np.zeros_like(m[t1]))).sum()
+        return m.sum() / (2 * union)
+
+    m = sel.cpu().numpy()[0]
+    aligned = m.copy()
+    for tp in range((blocks + 1) // 2):
+        t1, t2 = blocks - 1 - 2 * tp, blocks - 2 - 2 * tp
+        if t2 >= 0:
+            row = m[t1].copy()
+            row[t2 + 1:] = False
+            row[t2] = True
+            aligned[t2] = row
+    i2, c2 = kernels.indices_from_mask(torch.from_numpy(aligned[None]).cuda())
+    for label, lists, mask in (("routed", (idx, cnt), m), ("pair-aligned", (i2, c2), aligned)):
+        ms = timed(*lists)
+        n_sel = int(mask.sum())
+        print(json.dumps({"sweep": "pair-overlap", "lists": label, "seq": seq, "alpha": alpha,
+                          "qk_scale": qk_scale, "ms": round(ms, 3), "selected_tiles": n_sel,
+                          "union_efficiency": round(float(union_efficiency(mask)), 3),
+                          "pflops_on_selected": round(8388608 * n_sel / ms / 1e12, 3)}),
+              flush=True)
 
 
 def qwen2_7b_config(layers):
@@ -325,6 +386,11 @@ def main(argv=None) -> int:
     d2 = sub.add_parser("d256")
     d2.add_argument("--seq", type=int, default=32640)
     d2.add_argument("--seed", type=int, default=17)
+    po = sub.add_parser("pair-overlap")
+    po.add_argument("--seq", type=int, default=32640)
+    po.add_argument("--seed", type=int, default=17)
+    po.add_argument("--qk-scale", type=float, default=4.0)
+    po.add_argument("--alpha", type=float, default=0.7)
     mo = sub.add_parser("model")
     mo.add_argument("--seq", type=int, default=32640)
     mo.add_argument("--layers", type=int, default=28)
@@ -343,6 +409,8 @@ def main(argv=None) -> int:
         run_sparse(args.seq, args.seed, args.qk_scale)
     elif args.cmd == "d256":
         run_d256(args.seq, args.seed)
+    elif args.cmd == "pair-overlap":
+        run_pair_overlap(args.seq, args.seed, args.qk_scale, args.alpha)
     elif args.cmd == "long":
         cases = [("cgf_mean", 0.04), ("dispersion_mean", 0.04), ("mean_native", 0.04)]
         run_layer_sweep(args.seq, args.needles, args.seed, cases, "long")
