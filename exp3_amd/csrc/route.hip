@@ -244,20 +244,22 @@ template <int D> struct V1Ring {
   static_assert(kInFlight == 2 || kInFlight == 4, "ring waits below cover 2 or 4 loads");
 };
 
-// One 16-byte unit per lane, landing at lds_byte + 16 * lane (lds_byte wave-uniform).
+// One 16-byte unit per lane from base + byte_off (base wave-uniform, a 32-bit
+// per-lane offset), landing at lds_byte + 16 * lane (lds_byte wave-uniform).
 // Issued from assembly: the compiler's builtin for this load makes it treat all of
 // LDS as pending and wait for every copy before the next LDS read.
-__device__ __forceinline__ void v1_copy_unit(const uint16_t* src, uint32_t lds_byte) {
+__device__ __forceinline__ void v1_copy_unit(const uint16_t* base, uint32_t byte_off,
+                                             uint32_t lds_byte) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_byte);
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %1\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "s"(m0), "v"(src)
+      : "s"(m0), "v"(byte_off), "s"(base)
       : "memory");
 }
 template <int N> __device__ __forceinline__ void v1_wait_ring() {
@@ -300,6 +302,7 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   // L of a wave's i-th copy fills unit P = (4 i + wave) 64 + L of the slot; block
   // rows past the last block read the last block (masked out in the reduction).
   const uint16_t* kb_bg = a.kbar + b * a.ms_b + g * a.ms_h;
+  const int block_stride = (int)a.ms_j;   // elements between blocks (checked to fit on the host)
   const uint32_t ring_lds = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)&ring[0][0];
   auto issue_chunk = [&](int jc) {
     const uint32_t slot_lds = ring_lds + (uint32_t)((jc % R) * Ring::kSlotElems * 2);
@@ -310,7 +313,7 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
       const int r = unit / Ring::kUnitsPerRow;
       const int lu = (unit % Ring::kUnitsPerRow) ^ (r & 15);
       const int j = min(jc * 32 + r, nb - 1);
-      v1_copy_unit(kb_bg + (int64_t)j * a.ms_j + lu * 8, slot_lds + (uint32_t)p0 * 16u);
+      v1_copy_unit(kb_bg, (uint32_t)(j * block_stride + lu * 8) * 2u, slot_lds + (uint32_t)p0 * 16u);
     }
   };
   const int nchunks = (t + 1 + 31) / 32;
@@ -338,12 +341,15 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   const int hc = half ^ (col & 15);
   auto process = [&](int jc) {
     const uint16_t* slot = &ring[jc % R][col * D];
+    // every operand read issued before the dependent product chain starts
+    bf16x8 kbv[kSteps];
+#pragma unroll
+    for (int dc = 0; dc < kSteps; ++dc)
+      kbv[dc] = *reinterpret_cast<const bf16x8*>(slot + ((2 * dc) ^ hc) * 8);
+    __builtin_amdgcn_sched_barrier(0);
     f32x16 acc = {};
 #pragma unroll
-    for (int dc = 0; dc < kSteps; ++dc) {
-      const bf16x8 kb = *reinterpret_cast<const bf16x8*>(slot + ((2 * dc) ^ hc) * 8);
-      acc = mfma32(qa[dc], kb, acc);
-    }
+    for (int dc = 0; dc < kSteps; ++dc) acc = mfma32(qa[dc], kbv[dc], acc);
     // acc[r] = S[row 8*(r/4) + 4*half + r%4 of this wave][block j]
     const int j = jc * 32 + col;  // this lane's block column
     float mx, mass;
@@ -366,12 +372,10 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
 #pragma unroll
       for (int w = 1; w < 8; ++w) m = fmaxf(m, part_max[jc & 1][w][tid]);
       float s2 = 0.0f;
-      if (m != -INFINITY) {
+      if (m != -INFINITY) {   // a partial with no valid row has max -inf: 2^-inf = 0, mass 0
 #pragma unroll
-        for (int w = 0; w < 8; ++w) {
-          const float pm = part_max[jc & 1][w][tid];
-          if (pm != -INFINITY) s2 += part_mass[jc & 1][w][tid] * exp2_fast(pm - m);
-        }
+        for (int w = 0; w < 8; ++w)
+          s2 += part_mass[jc & 1][w][tid] * exp2_fast(part_max[jc & 1][w][tid] - m);
       }
       blk_max[jj] = m;
       blk_mass[jj] = s2;
@@ -548,6 +552,10 @@ static int v1_common(const void* q, const int64_t* q_strides, const void* mean_k
   if (e) return e;
   e = check_q("mean_k", mean_k, mk_strides);
   if (e) return e;
+  // the block-mean copies address a block by a 32-bit byte offset from its (b, g) base
+  SPX_REQUIRE(mk_strides[1] > 0 && (int64_t)blocks * mk_strides[1] * 2 < (1ll << 31), SPX_EINVAL,
+              "mean_k: block stride %lld must be positive and keep %d blocks within 2 GiB",
+              (long long)mk_strides[1], blocks);
   a->q = static_cast<const uint16_t*>(q);
   a->qs_b = q_strides[0]; a->qs_s = q_strides[1]; a->qs_h = q_strides[2];
   a->kbar = static_cast<const uint16_t*>(mean_k);
