@@ -30,7 +30,8 @@ constexpr int kSub = 32;                   // keys per sub-block
 constexpr int kSubElems = kSub * kD2;      // 8192 bf16 = 16 KB
 constexpr int kA2Threads = 256;
 constexpr int kA2MaxBlocks = 1024;
-constexpr float kLazy = 8.0f;              // log2 headroom before a column's running max moves
+constexpr float kLazy = 64.0f;             // log2 headroom before a column's running max moves
+                                           // (bf16 P, fp32 O and l: 2^64 loses nothing)
 
 // acc + lo + hi of a packed bf16 pair (v_dot2_f32_bf16 with (1, 1), from assembly:
 // the compiler's dot2 builtin lowering reads the wrong register when several of

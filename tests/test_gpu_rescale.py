@@ -2,12 +2,12 @@
 
 The keys of block j are c_j u plus noise and every query is 4 u plus noise (u a
 unit direction per kv group), so a key block's scores sit near 0.51 c_j in log2
-units. Step patterns of c_j make the running max jump by about 8 to 12 log2
+units. Step patterns of c_j make the running max jump by about 70 to 100 log2
 units from one block to the next (rising, rising then falling, alternating),
-so the full-block pipeline takes its rare rescale branch at block after block,
-and the masked diagonal path at the end sees maxima below, near and above the
-running one. All causal blocks are listed; outputs and LSE are compared with
-the oracle."""
+beyond the kernels' 2^64 lazy headroom, so the full-block pipeline takes its
+rare rescale branch at block after block, and the masked diagonal path at the
+end sees maxima below, near and above the running one. All causal blocks are
+listed; outputs and LSE are compared with the oracle."""
 
 import numpy as np
 import pytest
@@ -25,10 +25,10 @@ LENGTH = 1089   # 9 blocks, the last one partial
 def _pattern(name, blocks):
     j = np.arange(blocks)
     if name == "rising":
-        return 2.0 + 18.0 * j
+        return 2.0 + 160.0 * j
     if name == "peak":
-        return 2.0 + 24.0 * np.minimum(j, blocks - 1 - j)
-    return 2.0 + 24.0 * (j % 2)          # alternating
+        return 2.0 + 192.0 * np.minimum(j, blocks - 1 - j)
+    return 2.0 + 192.0 * (j % 2)         # alternating
 
 
 def _inputs(name, q_heads, kv_heads, dim, seed):
@@ -59,8 +59,9 @@ def test_exact_attention_rescale_patterns(gpu, pattern, shape):
     out, lse = up.exact_attention(q.cuda(), k.cuda(), v.cuda(), torch.from_numpy(idx).cuda(),
                                   torch.from_numpy(cnt).cuda(), scale)
     e_out, e_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, scale)
-    # the jumps are real: neighbouring blocks' score maxima differ by more than 2^8
+    # the jumps are real: neighbouring blocks' score maxima differ by more than the
+    # kernels' 2^64 headroom
     x = to_np(q)[0, -1, 0] @ to_np(k)[0, :blocks * 128 - 128 + 1:128, 0].T * scale / np.log(2)
-    assert np.abs(np.diff(x)).max() > 8.0
+    assert np.abs(np.diff(x)).max() > 64.0
     assert_output_close(to_np(out), e_out, what=f"{pattern} d={dim}")
     np.testing.assert_allclose(to_np(lse), e_lse, atol=0.02, rtol=0.01)
