@@ -30,7 +30,7 @@
 //     lands while block u is computed.
 //   * Full blocks are software-pipelined over their four 32-key sub-blocks (matrix
 //     work of one sub-block around the exponentials of the previous one); the
-//     running max moves lazily (only by more than 2^8), so the O rescale is a
+//     running max moves lazily (only by more than 2^64), so the O rescale is a
 //     rarely taken wave-uniform branch. The diagonal blocks (t and t - 1) run last
 //     through a masked path in which wave w touches only key sub-blocks 0 .. w.
 //   * Grid order: (tile pair, kv group) items heaviest-first, and the heads of one
@@ -48,10 +48,10 @@ constexpr int kMaxBlocksAttn = 1024;
 constexpr int kTailTile = 64;        // mean keys per tail tile (hi and lo rows fill K LDS)
 // log2 headroom before a column's running max moves. P is bf16 and O, l are fp32, all
 // with an 8-bit exponent, so probabilities up to 2^64 lose nothing; O then keeps
-// 2^128 / (2^64 * 2^15 keys) = 2^49 of headroom for |v|. Sharp score profiles
-// (routed sparse layers) move a column's maximum by tens of log2 units from block
-// to block: at a headroom of 2^8 the rescale branch ran in about half of a sparse
-// layer's sub-blocks, at 2^64 in under 3 %.
+// 2^128 / (2^64 * 2^17 keys at the 131072-token limit) = 2^47 of headroom for |v|.
+// Sharp score profiles (routed sparse layers) move a column's maximum by tens of
+// log2 units from block to block: at a headroom of 2^8 the rescale branch ran in
+// about half of a sparse layer's sub-blocks, at 2^64 in under 3 %.
 constexpr float kLazyRescale = 64.0f;
 
 struct AttnArgs {
@@ -313,7 +313,7 @@ __device__ __forceinline__ void exact_block(const uint16_t* kb, const uint16_t* 
 //
 // Sub-block 3's P V product stays pending in registers across the next block's
 // barrier. The running max moves lazily per sub-block (only when a column's
-// shifted max exceeds 2^8); the rescale of O comes after the P V products that
+// shifted max exceeds 2^64); the rescale of O comes after the P V products that
 // used the old max were issued and before any that use the new one.
 //
 // LDS operand addresses: entry c of a table is the byte address of 16-byte chunk
@@ -386,7 +386,7 @@ __device__ __forceinline__ void sub_pv(const bf16x8 (&r)[8], const bf16x8 (&p)[2
 // 16 keys of its column) and check them against the running max. The max runs
 // over the shifted values: results of arithmetic, which the compiler's max takes
 // without quieting them first. The running max moves lazily: only when a
-// column's x exceeds ws.thr (2^8 once set); then (rarely) O and l are rescaled
+// column's x exceeds ws.thr (2^64 once set); then (rarely) O and l are rescaled
 // and x shifted by the same amount. Before the first move neg_m is 0 and thr
 // -inf, so the first sub-block sets the max from its own scores. The common path
 // checks each lane half's own max; the column max over both halves is formed
@@ -673,7 +673,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
       count = min(max(count, 0), a.blocks);
       const int64_t* list = a.idx + b * a.is_b + tt * a.is_t + h * a.is_h;
       for (int pos = tid; pos < count; pos += kAttnThreads) {
-        const int j = (int)list[pos * a.is_p];
+        const int64_t j = list[pos * a.is_p];   // range-checked before narrowing
         if (j >= 0 && j < a.blocks) atomicAdd(&mult[it][j >> 1], 1u << ((j & 1) * 16));
       }
     } else {

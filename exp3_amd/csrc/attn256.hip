@@ -16,7 +16,7 @@
 //     k-steps), so each lane owns one query column: the online softmax is in-lane
 //     plus one lane-half exchange, and the probabilities already sit in the B-operand
 //     layout of O^T += V^T P^T (key slot permutation of the value tiles). The running
-//     max moves only when a column's shifted score x = s * scale - m exceeds 2^8
+//     max moves only when a column's shifted score x = s * scale - m exceeds 2^64
 //     (lazy rescale); the common path checks each lane half's own max of x.
 //   * The tile's list (entries outside [0, NB) skipped, as the reference's loop
 //     never reads them usefully) is compacted into LDS once; as in the reference,
@@ -103,12 +103,12 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
     int base = 0;
     for (int u0 = 0; u0 < n; u0 += 64) {
       const int u = u0 + lane;
-      int j = -1;
-      if (u < n) j = a.idx ? (int)a.idx[b * a.is_b + t * a.is_t + u * a.is_p + h * a.is_h] : u;
+      int64_t j = -1;   // range-checked before narrowing
+      if (u < n) j = a.idx ? a.idx[b * a.is_b + t * a.is_t + u * a.is_p + h * a.is_h] : u;
       const bool ok = j >= 0 && j < a.blocks;
       const uint64_t m = __ballot(ok);
       const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
-      if (ok) list[pos] = j;
+      if (ok) list[pos] = (int)j;
       base += __popcll(m);
     }
     if (lane == 0) list_len = base;

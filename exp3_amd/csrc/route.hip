@@ -341,15 +341,20 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   const int hc = half ^ (col & 15);
   auto process = [&](int jc) {
     const uint16_t* slot = &ring[jc % R][col * D];
-    // every operand read issued before the dependent product chain starts
-    bf16x8 kbv[kSteps];
-#pragma unroll
-    for (int dc = 0; dc < kSteps; ++dc)
-      kbv[dc] = *reinterpret_cast<const bf16x8*>(slot + ((2 * dc) ^ hc) * 8);
-    __builtin_amdgcn_sched_barrier(0);
+    // operand reads issued a group of k-steps ahead of the dependent product chain;
+    // groups of at most 8 (32 registers) keep d = 256 at three waves per SIMD
+    constexpr int kGroup = kSteps < 8 ? kSteps : 8;
     f32x16 acc = {};
 #pragma unroll
-    for (int dc = 0; dc < kSteps; ++dc) acc = mfma32(qa[dc], kbv[dc], acc);
+    for (int g0 = 0; g0 < kSteps; g0 += kGroup) {
+      bf16x8 kbv[kGroup];
+#pragma unroll
+      for (int i = 0; i < kGroup; ++i)
+        kbv[i] = *reinterpret_cast<const bf16x8*>(slot + ((2 * (g0 + i)) ^ hc) * 8);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < kGroup; ++i) acc = mfma32(qa[g0 + i], kbv[i], acc);
+    }
     // acc[r] = S[row 8*(r/4) + 4*half + r%4 of this wave][block j]
     const int j = jc * 32 + col;  // this lane's block column
     float mx, mass;

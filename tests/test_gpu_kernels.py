@@ -273,6 +273,9 @@ def test_exact_attention_edge_lists(gpu):
     idx[0, 2, 0, 5] = 2      # diagonal + an out-of-range id
     idx[0, 2, 1, 5] = 99
     cnt[0, 2, 5] = 2
+    # ids whose low 32 bits are in range are still out of range (no narrowing)
+    idx[0, 2, :3, 7] = [(1 << 32) + 1, 2, -(1 << 32) + 1]
+    cnt[0, 2, 7] = 3
     out, lse = up.exact_attention(qg, kg, vg, torch.from_numpy(idx).cuda(),
                                   torch.from_numpy(cnt).cuda(), SCALE)
     e_out, e_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE)
