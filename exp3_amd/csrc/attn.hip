@@ -33,9 +33,11 @@
 //     running max moves lazily (only by more than 2^64), so the O rescale is a
 //     rarely taken wave-uniform branch. The diagonal blocks (t and t - 1) run last
 //     through a masked path in which wave w touches only key sub-blocks 0 .. w.
-//   * Grid order: (tile pair, kv group) items heaviest-first, and the heads of one
-//     group consecutive on the same XCD (workgroup i runs on XCD i % 8), so the
-//     seven q heads sharing a KV block read it from the same L2.
+//   * Grid order: (tile pair, q head) items heaviest-first. Workgroup i runs on XCD
+//     i % 8; a (batch, kv group) stream is served by a fixed set of XCDs, so the q
+//     heads sharing a KV block read it from the same L2s, and with 8 / (B * Hkv)
+//     XCDs per stream the heads of each tile pair are dealt over that set in turn,
+//     which keeps the XCDs' shares of the work equal.
 #include <type_traits>
 
 #include "common.h"
@@ -75,6 +77,7 @@ struct AttnArgs {
   float* lse;  // nullable
   int64_t ls_b, ls_s, ls_h;
   int batch, seq, q_heads, kv_heads, blocks, group, num_pairs;
+  int xcds_per_stream;   // XCDs sharing one (batch, kv group) stream; 1: pair p on XCD p % 8
   float scale_log2;
 };
 
@@ -600,17 +603,32 @@ __device__ __forceinline__ void stage_rescue(const AttnArgs& a, const int16_t* i
 
 template <bool EXACT, bool TAIL, bool OUT_F32>
 __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
-  // ---- work item: query tiles (t, t - 1) of one q head. Tile pairs heaviest first,
-  // the heads of one kv group consecutive on the same XCD (workgroup i runs on
-  // XCD i % 8) so the seven q heads sharing a KV block read it from one L2.
+  // ---- work item: query tiles (t, t - 1) of one q head. Tile pairs heaviest first;
+  // workgroup i runs on XCD i % 8, and each XCD serves one (batch, kv group) stream
+  // (or a few when there are more than 8), so the q heads sharing a KV block read
+  // it from one L2.
   const int p = blockIdx.x;
   const int xcd = p & 7;
   const int local = p >> 3;
-  const int pair_local = local / a.group;
-  const int hg = local - pair_local * a.group;
-  const int pair = pair_local * 8 + xcd;
-  if (pair >= a.num_pairs) return;
   const int bg = a.batch * a.kv_heads;
+  int pair, hg;
+  if (a.xcds_per_stream > 1) {
+    // (batch, kv group) stream s runs on the xcds_per_stream XCDs x = s (mod bg); its
+    // items k = tp * group + hg (heaviest first) are dealt over them in turn, so the
+    // heads of a tile pair alternate between those XCDs and every XCD's share of
+    // each stream is balanced (one stream per XCD would give it every other tile
+    // pair, and the always-full last tiles all to the same XCDs)
+    const int s = xcd % bg;
+    const int k = local * a.xcds_per_stream + xcd / bg;
+    const int tpk = k / a.group;
+    hg = k - tpk * a.group;
+    pair = tpk * bg + s;
+  } else {
+    const int pair_local = local / a.group;
+    hg = local - pair_local * a.group;
+    pair = pair_local * 8 + xcd;
+  }
+  if (pair >= a.num_pairs) return;
   const int tp = pair / bg;                          // tile pair: tiles NB-1-2tp, NB-2-2tp
   const int b = (pair % bg) / a.kv_heads;
   const int g = (pair % bg) % a.kv_heads;
@@ -1029,7 +1047,12 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
   a.blocks = blocks; a.group = q_heads / kv_heads;
   a.num_pairs = ((blocks + 1) / 2) * batch * kv_heads;  // (tile pair, batch, kv group)
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
-  const int grid = ((a.num_pairs + 7) / 8) * 8 * a.group;
+  const int streams = batch * kv_heads;
+  a.xcds_per_stream = (streams <= 8 && 8 % streams == 0) ? 8 / streams : 1;
+  const int per_xcd = a.xcds_per_stream > 1
+      ? ((blocks + 1) / 2 * a.group + a.xcds_per_stream - 1) / a.xcds_per_stream
+      : (a.num_pairs + 7) / 8 * a.group;
+  const int grid = 8 * per_xcd;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (req.exact && !req.tail) attn_kernel<true, false, false><<<grid, kAttnThreads, 0, st>>>(a);
   else if (req.exact && req.tail) attn_kernel<true, true, false><<<grid, kAttnThreads, 0, st>>>(a);

@@ -22,6 +22,16 @@
       fp_v1 on sharpened inputs: the attention kernel on the routed lists and on
       lists where each tile pair's lists coincide (tile t - 1 takes tile t's routed
       blocks), the cost of pairing tiles whose lists differ
+  python -m measure.sweeps cost-model [--seq 32640]
+      the attention kernel on synthetic lists (unscaled inputs): every list empty,
+      then k blocks per tile pair listed by both tiles or by one tile only; prints
+      each case's time and the fitted per-workgroup and per-step costs
+  python -m measure.sweeps xcd-balance [--seq 32640] [--qk-scale 4] [--alpha 0.7]
+      routes the fp_v1 layer on the GPU, then simulates on the CPU how the
+      attention grid's work items land on the 8 XCDs (workgroup i on XCD i % 8,
+      greedy dispatch to each XCD's CUs in grid order) under the shipped mapping
+      and the earlier one-tile-pair-per-XCD mapping, with per-item costs from
+      the cost model; also for the dense (all causal blocks) lists
   python -m measure.sweeps model [--seq 32640] [--layers 28] [--repeats 3]
       full prefill of a random-init Qwen2.5-7B-shaped model built from a local
       config (28 layers, hidden 3584, FFN 18944, 28/4 heads, RMSNorm 1e-6,
@@ -195,6 +205,158 @@ def run_pair_overlap(seq, seed, qk_scale, alpha):
                           "union_efficiency": round(float(union_efficiency(mask)), 3),
                           "pflops_on_selected": round(8388608 * n_sel / ms / 1e12, 3)}),
               flush=True)
+
+
+def _attention_timer(torch, backend, q, k, tiles, scale):
+    def timed(indices, counts, n=10):
+        for _ in range(3):
+            backend._attention(q, k, tiles, indices, counts, scale, None)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            backend._attention(q, k, tiles, indices, counts, scale, None)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+    return timed
+
+
+def run_cost_model(seq, seed):
+    """Per-workgroup and per-step costs of the attention kernel from synthetic lists:
+    every list empty (fixed cost: Q in, O out, list merge), then for each tile pair
+    (t, t - 1) the k most recent history blocks below t - 1 listed by both tiles
+    (shared steps) or by tile t only (one-sided steps), diagonals as routing lists
+    them. Per-step costs are the slope between k = 16 and k = 32."""
+    import numpy as np
+    import torch
+    from exp3_amd import _lib, attention, synthetic
+    _lib.load()
+    q, k, v, _ = synthetic.make_inputs(seq, seed=seed, device="cuda")
+    scale = 128 ** -0.5
+    b = attention.AttentionBackend(alpha=0.08, register=False)
+    b.configure("fp_v1", 0.08)
+    _, _, tiles, _, _, _, sel = b._route_v1(q, k, v, scale, {"events": {}}, False, True)
+    blocks, heads = sel.shape[1], sel.shape[3]
+    timed = _attention_timer(torch, b, q, k, tiles, scale)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    workgroups = (blocks + 1) // 2 * heads
+
+    def lists(kk, mode):
+        ind = np.full((blocks, blocks, heads), blocks, dtype=np.int64)
+        cnt = np.zeros((blocks, heads), dtype=np.int32)
+        union = 0
+        for tp in range((blocks + 1) // 2):
+            t1, t2 = blocks - 1 - 2 * tp, blocks - 2 - 2 * tp
+            lim = max(t2, 0)
+            hist = list(range(lim - min(kk, lim), lim))
+            l1 = [] if mode == "empty" else hist + ([t2] if t2 >= 0 else []) + [t1]
+            l2 = [] if mode == "empty" else (hist if mode == "shared" else []) + [t2]
+            ind[t1, :len(l1)] = np.array(l1, dtype=np.int64)[:, None] if l1 else blocks
+            cnt[t1] = len(l1)
+            if t2 >= 0:
+                ind[t2, :len(l2)] = np.array(l2, dtype=np.int64)[:, None] if l2 else blocks
+                cnt[t2] = len(l2)
+            union += heads * len(set(l1) | (set(l2) if t2 >= 0 else set()))
+        return torch.from_numpy(ind[None]).cuda(), torch.from_numpy(cnt[None]).cuda(), union
+
+    rows = {}
+    for mode, kk in (("empty", 0), ("shared", 16), ("shared", 32), ("one-sided", 16),
+                     ("one-sided", 32)):
+        i, c, union = lists(kk, mode)
+        ms = timed(i, c, 20)
+        rows[(mode, kk)] = (ms, union)
+        print(json.dumps({"sweep": "cost-model", "lists": mode, "k": kk, "ms": round(ms, 4),
+                          "steps": union, "selected_tiles": int(c.sum().item())}), flush=True)
+    slope = lambda m: ((rows[(m, 32)][0] - rows[(m, 16)][0])
+                       / (rows[(m, 32)][1] - rows[(m, 16)][1]) * 1e6)   # ns per step, GPU-wide
+    fit = {"sweep": "cost-model-fit", "cus": cus, "workgroups": workgroups,
+           "fixed_us_per_workgroup": round(rows[("empty", 0)][0] * 1e3 * cus / workgroups, 2),
+           "shared_step_ns": round(slope("shared"), 2),
+           "one_sided_step_ns": round(slope("one-sided"), 2)}
+    fit["shared_step_us_per_cu"] = round(fit["shared_step_ns"] * cus / 1e3, 3)
+    fit["one_sided_step_us_per_cu"] = round(fit["one_sided_step_ns"] * cus / 1e3, 3)
+    print(json.dumps(fit), flush=True)
+
+
+def attention_grid_items(batch, kv_heads, group, blocks, alternating=True):
+    """Work items (tile pair, batch, kv group, head in group) of the d = 128 attention
+    grid per XCD, in grid order, as the kernel maps workgroup i (XCD i % 8): with
+    ``alternating`` the shipped mapping (a (batch, kv group) stream on 8 / (B Hkv)
+    XCDs, its items dealt over them in turn), else pair p on XCD p % 8 with all its
+    heads."""
+    pairs_per_stream = (blocks + 1) // 2
+    streams = batch * kv_heads
+    num_pairs = pairs_per_stream * streams
+    per_stream = 8 // streams if alternating and streams <= 8 and 8 % streams == 0 else 1
+    if per_stream > 1:
+        per_xcd = (pairs_per_stream * group + per_stream - 1) // per_stream
+    else:
+        per_xcd = (num_pairs + 7) // 8 * group
+    out = [[] for _ in range(8)]
+    for p in range(8 * per_xcd):
+        xcd, local = p & 7, p >> 3
+        if per_stream > 1:
+            kk = local * per_stream + xcd // streams
+            pair, hg = (kk // group) * streams + xcd % streams, kk % group
+        else:
+            pair, hg = (local // group) * 8 + xcd, local % group
+        if pair < num_pairs:
+            tp, s = pair // streams, pair % streams
+            out[xcd].append((tp, s // kv_heads, s % kv_heads, hg))
+    return out
+
+
+def simulate_xcds(mask, kv_heads, costs, alternating, cus_per_xcd=32):
+    """Greedy dispatch of each XCD's items to its CUs in grid order; returns
+    (makespan, per-XCD work per CU, ideal) in the unit of ``costs`` (fixed per
+    item, per shared step, per one-sided step)."""
+    import heapq
+    import numpy as np
+    blocks, _, heads = mask.shape
+    group = heads // kv_heads
+    fixed, shared, one = costs
+    loads, spans = [], []
+    for items in attention_grid_items(1, kv_heads, group, blocks, alternating):
+        heap = [0.0] * cus_per_xcd
+        total = 0.0
+        for tp, _, g, hg in items:
+            h = g * group + hg
+            t1, t2 = blocks - 1 - 2 * tp, blocks - 2 - 2 * tp
+            a = mask[t1, :, h]
+            bb = mask[t2, :, h] if t2 >= 0 else np.zeros(blocks, bool)
+            c = fixed + shared * int((a & bb).sum()) + one * int((a ^ bb).sum())
+            total += c
+            heapq.heappush(heap, heapq.heappop(heap) + c)
+        loads.append(total / cus_per_xcd)
+        spans.append(max(heap))
+    return max(spans), loads, sum(loads) / 8
+
+
+def run_xcd_balance(seq, seed, qk_scale, alpha, costs):
+    import numpy as np
+    import torch
+    from exp3_amd import _lib, attention, synthetic
+    _lib.load()
+    q, k, v, _ = synthetic.make_inputs(seq, seed=seed, device="cuda")
+    q = (q.float() * qk_scale).to(torch.bfloat16)
+    k = (k.float() * qk_scale).to(torch.bfloat16)
+    b = attention.AttentionBackend(alpha=alpha, register=False)
+    b.configure("fp_v1", alpha)
+    _, _, _, _, _, _, sel = b._route_v1(q, k, v, 128 ** -0.5, {"events": {}}, False, False)
+    routed = sel.cpu().numpy()[0]
+    blocks, _, heads = routed.shape
+    dense = np.broadcast_to(np.tril(np.ones((blocks, blocks), bool))[:, :, None],
+                            routed.shape)
+    kv_heads = k.shape[2]
+    for label, mask in (("fp_v1 routed", routed), ("dense", dense)):
+        for alternating in (False, True):
+            span, loads, ideal = simulate_xcds(mask, kv_heads, costs, alternating)
+            print(json.dumps({"sweep": "xcd-balance", "lists": label, "alpha": alpha,
+                              "qk_scale": qk_scale,
+                              "mapping": "alternating heads" if alternating else "pair per XCD",
+                              "makespan_ms": round(span / 1e3, 3), "ideal_ms": round(ideal / 1e3, 3),
+                              "per_xcd_ms": [round(x / 1e3, 3) for x in loads]}), flush=True)
 
 
 def qwen2_7b_config(layers):
@@ -391,6 +553,16 @@ def main(argv=None) -> int:
     po.add_argument("--seed", type=int, default=17)
     po.add_argument("--qk-scale", type=float, default=4.0)
     po.add_argument("--alpha", type=float, default=0.7)
+    cm = sub.add_parser("cost-model")
+    cm.add_argument("--seq", type=int, default=32640)
+    cm.add_argument("--seed", type=int, default=17)
+    xb = sub.add_parser("xcd-balance")
+    xb.add_argument("--seq", type=int, default=32640)
+    xb.add_argument("--seed", type=int, default=17)
+    xb.add_argument("--qk-scale", type=float, default=4.0)
+    xb.add_argument("--alpha", type=float, default=0.7)
+    xb.add_argument("--costs", default="12.6,3.45,2.02",
+                    help="microseconds per CU: fixed per workgroup, shared step, one-sided step")
     mo = sub.add_parser("model")
     mo.add_argument("--seq", type=int, default=32640)
     mo.add_argument("--layers", type=int, default=28)
@@ -411,6 +583,11 @@ def main(argv=None) -> int:
         run_d256(args.seq, args.seed)
     elif args.cmd == "pair-overlap":
         run_pair_overlap(args.seq, args.seed, args.qk_scale, args.alpha)
+    elif args.cmd == "cost-model":
+        run_cost_model(args.seq, args.seed)
+    elif args.cmd == "xcd-balance":
+        run_xcd_balance(args.seq, args.seed, args.qk_scale, args.alpha,
+                        tuple(float(x) for x in args.costs.split(",")))
     elif args.cmd == "long":
         cases = [("cgf_mean", 0.04), ("dispersion_mean", 0.04), ("mean_native", 0.04)]
         run_layer_sweep(args.seq, args.needles, args.seed, cases, "long")

@@ -1,5 +1,6 @@
-"""CPU checks of the measurement helpers: the rocprofv3 traffic reduction and the
-full-model sweep's Qwen2.5-7B-shaped config (no GPU needed)."""
+"""CPU checks of the measurement helpers: the rocprofv3 traffic reduction, the
+full-model sweep's Qwen2.5-7B-shaped config and the CPU mirror of the attention
+grid's XCD mapping (no GPU needed)."""
 
 import csv
 import json
@@ -84,3 +85,40 @@ def test_bench_cpu_baseline_layer_equals_oracle_layer(method):
     np.testing.assert_array_equal(out, expected["output"])
     sampled = bench._oracle_tiles(ref, qn, kn, vn, SCALE, method, route, [1])
     np.testing.assert_array_equal(sampled[:, 128:256], expected["output"][:, 128:256])
+
+
+@pytest.mark.parametrize("batch,kv_heads,group,blocks", [(1, 4, 7, 255), (1, 4, 7, 9), (2, 4, 7, 17),
+                                                         (1, 1, 8, 33), (1, 8, 4, 12), (3, 2, 6, 5)])
+@pytest.mark.parametrize("alternating", (False, True))
+def test_attention_grid_items_cover_every_item_once(batch, kv_heads, group, blocks, alternating):
+    """The CPU mirror of the attention kernel's workgroup -> (tile pair, head) mapping
+    deals every item to exactly one XCD, and when the number of (batch, kv group)
+    streams divides 8, XCD x serves stream x mod streams only."""
+    from measure import sweeps
+    per_xcd = sweeps.attention_grid_items(batch, kv_heads, group, blocks, alternating)
+    items = [it for lst in per_xcd for it in lst]
+    pairs = (blocks + 1) // 2
+    assert sorted(items) == sorted((tp, b, g, hg) for tp in range(pairs) for b in range(batch)
+                                   for g in range(kv_heads) for hg in range(group))
+    streams = batch * kv_heads
+    if 8 % streams == 0:
+        for xcd, lst in enumerate(per_xcd):
+            assert all((b * kv_heads + g) == xcd % streams for tp, b, g, hg in lst)
+
+
+def test_alternating_mapping_splits_tile_pairs_and_balances_xcds():
+    """With 4 kv groups the heads of each tile pair alternate between XCDs g and g + 4,
+    and on the dense lists every XCD gets the same work (the earlier mapping gave
+    XCDs 0-3 the heavier pair of every two)."""
+    import numpy as np
+    from measure import sweeps
+    per_xcd = sweeps.attention_grid_items(1, 4, 7, 255, True)
+    heads_of_pair0 = {x: sorted(hg for tp, b, g, hg in per_xcd[x] if tp == 0 and g == 0)
+                      for x in (0, 4)}
+    assert heads_of_pair0 == {0: [0, 2, 4, 6], 4: [1, 3, 5]}
+    dense = np.broadcast_to(np.tril(np.ones((255, 255), bool))[:, :, None], (255, 255, 28))
+    span_old, loads_old, ideal = sweeps.simulate_xcds(dense, 4, (12.6, 3.45, 2.02), False)
+    span_new, loads_new, ideal2 = sweeps.simulate_xcds(dense, 4, (12.6, 3.45, 2.02), True)
+    assert ideal == pytest.approx(ideal2)
+    assert max(loads_new) - min(loads_new) < 0.01 * ideal < max(loads_old) - min(loads_old)
+    assert span_new < span_old
