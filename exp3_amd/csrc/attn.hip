@@ -910,10 +910,11 @@ struct MergeArgs {
   int64_t os_b, os_s, os_h;
   float* lo;
   int64_t los_b, los_s, los_h;
-  int batch, seq, heads;
+  int batch, seq, heads, dim;
 };
 
-// One wave per (b, s, h) row of 128 dims; each lane handles 2 dims.
+// One wave per (b, s, h) row of dim (128 or 256) dims; each lane handles 2 dims per
+// 128.
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t rows = (int64_t)a.batch * a.seq * a.heads;
@@ -932,12 +933,15 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
   else total = mx + log1pf(expf(-fabsf(le - lm)));
   const float we = expf(le - total);
   const float wm = expf(lm - total);
-  const int d = lane * 2;
-  const uint32_t e2 = *reinterpret_cast<const uint32_t*>(a.eo + b * a.es_b + s * a.es_s + h * a.es_h + d);
-  const float* m2 = a.mo + b * a.ms_b + s * a.ms_s + h * a.ms_h + d;
-  const float o0 = bf16_lo(e2) * we + m2[0] * wm;
-  const float o1 = bf16_hi(e2) * we + m2[1] * wm;
-  *reinterpret_cast<uint32_t*>(a.out + b * a.os_b + s * a.os_s + h * a.os_h + d) = pack_bf16x2(o0, o1);
+  for (int d = lane * 2; d < a.dim; d += 128) {
+    const uint32_t e2 =
+        *reinterpret_cast<const uint32_t*>(a.eo + b * a.es_b + s * a.es_s + h * a.es_h + d);
+    const float* m2 = a.mo + b * a.ms_b + s * a.ms_s + h * a.ms_h + d;
+    const float o0 = bf16_lo(e2) * we + m2[0] * wm;
+    const float o1 = bf16_hi(e2) * we + m2[1] * wm;
+    *reinterpret_cast<uint32_t*>(a.out + b * a.os_b + s * a.os_s + h * a.os_h + d) =
+        pack_bf16x2(o0, o1);
+  }
   if (a.lo && lane == 0) a.lo[b * a.los_b + s * a.los_s + h * a.los_h] = total;
 }
 
@@ -975,9 +979,8 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
                      int batch, int seq, int q_heads, int kv_heads, int head_dim,
                      int block_size, float scale, void* out, const int64_t* out_strides,
                      float* lse, const int64_t* lse_strides, void* stream) {
-  SPX_REQUIRE(head_dim == kHeadDim || (head_dim == 256 && req.exact && !req.tail),
-              SPX_EUNSUPPORTED,
-              "head_dim %d unsupported (128; 256 for exact attention without a tail)", head_dim);
+  SPX_REQUIRE(head_dim == kHeadDim || head_dim == 256, SPX_EUNSUPPORTED,
+              "head_dim %d unsupported (128 or 256)", head_dim);
   SPX_REQUIRE(block_size == kBlock, SPX_EUNSUPPORTED, "block_size %d unsupported (only 128)", block_size);
   SPX_REQUIRE(batch > 0 && seq > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
               SPX_EINVAL, "bad shape: batch %d seq %d q_heads %d kv_heads %d", batch, seq,
@@ -1016,10 +1019,13 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
     SPX_REQUIRE(req.exact, SPX_EINVAL, "mean_tail needs index lists");
   }
   if (lse) SPX_REQUIRE(lse_strides != nullptr, SPX_EINVAL, "lse strides missing");
-  if (head_dim == 256)
-    return launch_attention_256(q, q_strides, key_tiles, value_tiles, indices, index_strides,
+  if (head_dim == 256) {
+    const Attn256Options opt{req.exact, req.tail, req.out_f32, req.tail_kind, mean_k, mean_v,
+                             block_counts, req.choice, req.v, req.v_strides};
+    return launch_attention_256(opt, q, q_strides, key_tiles, value_tiles, indices, index_strides,
                                 counts, count_strides, batch, seq, q_heads, kv_heads, scale, out,
                                 out_strides, lse, lse_strides, stream);
+  }
 
   AttnArgs a{};
   a.q = static_cast<const uint16_t*>(q);
@@ -1112,7 +1118,8 @@ extern "C" int spx_merge_exact_mean(const void* exact_out, const int64_t* exact_
                                     int batch, int seq, int heads, int head_dim, void* out,
                                     const int64_t* out_strides, float* lse_out,
                                     const int64_t* lse_out_strides, void* stream) {
-  SPX_REQUIRE(head_dim == kHeadDim, SPX_EUNSUPPORTED, "head_dim %d unsupported (only 128)", head_dim);
+  SPX_REQUIRE(head_dim == kHeadDim || head_dim == 256, SPX_EUNSUPPORTED,
+              "head_dim %d unsupported (128 or 256)", head_dim);
   SPX_REQUIRE(batch > 0 && seq > 0 && heads > 0, SPX_EINVAL, "bad shape");
   int e = check_bsdh("exact_out", exact_out, exact_strides, false);
   if (e) return e;
@@ -1141,7 +1148,7 @@ extern "C" int spx_merge_exact_mean(const void* exact_out, const int64_t* exact_
     SPX_REQUIRE(lse_out_strides != nullptr, SPX_EINVAL, "lse_out strides missing");
     a.los_b = lse_out_strides[0]; a.los_s = lse_out_strides[1]; a.los_h = lse_out_strides[2];
   }
-  a.batch = batch; a.seq = seq; a.heads = heads;
+  a.batch = batch; a.seq = seq; a.heads = heads; a.dim = head_dim;
   const int64_t rows = (int64_t)batch * seq * heads;
   const int grid = (int)((rows + 3) / 4);
   merge_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);

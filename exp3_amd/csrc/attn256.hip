@@ -21,6 +21,14 @@
 //   * The tile's list (entries outside [0, NB) skipped, as the reference's loop
 //     never reads them usefully) is compacted into LDS once; as in the reference,
 //     only the diagonal block j == t is masked (key > query).
+//   * Tails (mean methods, kernels.py:179-230 + :312-325; rescue methods,
+//     kernels.py:233-309), after the exact blocks inside the same online softmax:
+//     the history blocks j < t the tile does not list, 32 entries per sub-block,
+//     staged into LDS by all four waves. An entry's key is an fp32 vector (block
+//     mean, or (128 mean - token) / 127 for the rescue remainder) split into bf16
+//     hi and lo rows in the two K buffers, whose products are summed (fp32-accurate
+//     logits); its value is bf16 in the first V buffer; its logit bias (ln n_j, 0 or
+//     ln 127) is added after scaling. Exact keys (rescue tokens) have lo rows 0.
 #include "common.h"
 
 namespace spx {
@@ -52,11 +60,136 @@ struct Attn256Args {
   int64_t cs_b, cs_t, cs_h;
   int batch, seq, q_heads, kv_heads, blocks;
   float scale_log2;
-  uint16_t* out;
+  void* out;           // bf16, or fp32 for the tail-only entry points
   int64_t os_b, os_s, os_h;
   float* lse;
   int64_t ls_b, ls_s, ls_h;
+  // tails
+  int tail_kind;       // 0 block means, 1 rescue token, 2 rescue token + remainder
+  const float* mean_k; // [B, NB, Hkv, 256]
+  const float* mean_v;
+  const int32_t* bcounts;
+  const uint8_t* choice;
+  const uint16_t* v;
+  int64_t vs_b, vs_s, vs_h;
 };
+
+// Position of 16-byte chunk c (< 32) of K row r in the d = 256 key layout.
+__device__ __forceinline__ int key_chunk_pos(int r, int c) { return (c & 16) | ((c & 15) ^ (r & 15)); }
+
+// The rare branch of the lazy max and the probability / P V half of a 32-key
+// sub-block, on shifted scores x = s * scale (+ bias) - m (masked keys -inf).
+__device__ __forceinline__ void softmax_pv(f32x16& x, const uint16_t* vb, f32x16 (&o)[8],
+                                           float& neg_m, float& thr, float& l) {
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 31, half = lane >> 5;
+  const int vsw = (col >> 2) & 3;
+  float mx = fmaxf(fmaxf(x[0], x[1]), x[2]);
+#pragma unroll
+  for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, x[r]), x[r + 1]);
+  mx = fmaxf(mx, x[15]);
+  if (__any(mx > thr)) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                     false, false);
+    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    const bool move = mx > thr;
+    const float d = move ? mx : 0.0f;
+    // nothing is accumulated before the first move (thr -inf): O and l stay 0
+    const float corr = thr == -INFINITY ? 0.0f : exp2_fast(-d);
+    // in place (tied operands): O keeps its registers across the rare branch. The
+    // compiler's hazard recognizer does not look inside asm statements, so the
+    // wait states after the last product into O (19 >= the XDL write -> VALU
+    // requirement) are issued first, tied to O.
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 2"
+                 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(o[4]), "+v"(o[5]),
+                   "+v"(o[6]), "+v"(o[7]));
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(o[dt][r]) : "v"(corr));
+    l *= corr;
+    neg_m -= d;
+    if (move) thr = kLazy;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] -= d;
+  }
+  // probabilities as bf16 B operands; the running sum adds the rounded values
+  u32x4 pb0, pb1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    pb0[e] = pack_bf16x2(exp2_fast(x[2 * e]), exp2_fast(x[2 * e + 1]));
+    l = add_bf16_pair(l, pb0[e]);
+    pb1[e] = pack_bf16x2(exp2_fast(x[8 + 2 * e]), exp2_fast(x[8 + 2 * e + 1]));
+    l = add_bf16_pair(l, pb1[e]);
+  }
+#pragma unroll
+  for (int d2 = 0; d2 < 4; ++d2) {
+    bf16x8 vr[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint16_t* vrow = vb + ((2 * d2 + i) * 32 + col) * kSub;
+      vr[2 * i] = as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + ((half ^ vsw) << 3)));
+      vr[2 * i + 1] =
+          as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + (((2 + half) ^ vsw) << 3)));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      o[2 * d2 + i] = mfma32(vr[2 * i], as_bf16x8(pb0), o[2 * d2 + i]);
+      o[2 * d2 + i] = mfma32(vr[2 * i + 1], as_bf16x8(pb1), o[2 * d2 + i]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// S^T += K Q^T over the 16 k-steps of one 32-row K buffer; operand reads in groups
+// of four k-steps (fenced), so that at most four K operands are live: with O (128)
+// and Q (64) the wave stays under 256 VGPRs and O never leaves its registers.
+__device__ __forceinline__ void key_products(const uint16_t* kb, int e0, const bf16x8 (&qb)[16],
+                                             f32x16& sc) {
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4) {
+    bf16x8 kr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int dc = g4 * 4 + i;
+      kr[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(kb + (dc >> 3) * 128 +
+                                                          (e0 ^ ((dc & 7) << 4))));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc = mfma32(kr[i], qb[g4 * 4 + i], sc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+__device__ __forceinline__ void load8f(const float* p, float (&x)[8]) {
+  const f32x4 a0 = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 a1 = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { x[e] = a0[e]; x[4 + e] = a1[e]; }
+}
+
+// Tail sub-block entry i (< 32), 8-dim chunk c (< 32): key hi / lo rows in kh / kl,
+// value in slot value_slot_of_key(i) of dim rows 8c .. 8c + 7 of vb.
+__device__ __forceinline__ void write_tail_entry256(uint16_t* kh, uint16_t* kl, uint16_t* vb,
+                                                   int i, int c, const float (&mk)[8],
+                                                   const float (&mv)[8]) {
+  u32x4 hi, lo;
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const uint32_t h2 = pack_bf16x2(mk[2 * x], mk[2 * x + 1]);
+    hi[x] = h2;
+    lo[x] = pack_bf16x2(mk[2 * x] - bf16_lo(h2), mk[2 * x + 1] - bf16_hi(h2));
+  }
+  const int koff = i * kD2 + key_chunk_pos(i, c) * 8;
+  *reinterpret_cast<u32x4*>(kh + koff) = hi;
+  *reinterpret_cast<u32x4*>(kl + koff) = lo;
+  const int slot = value_slot_of_key(i);
+#pragma unroll
+  for (int x = 0; x < 8; ++x) {
+    const int d = c * 8 + x;
+    vb[d * kSub + ((((slot >> 3) ^ ((d >> 2) & 3))) << 3) + (slot & 7)] = to_bf16_bits(mv[x]);
+  }
+}
 
 // 16 KB from global memory into LDS: four instructions of 256 lanes x 16 bytes.
 __device__ __forceinline__ void dma_16k(const uint16_t* src, uint16_t* lds, int tid) {
@@ -82,6 +215,7 @@ __device__ __forceinline__ void dma_16k(const uint16_t* src, uint16_t* lds, int 
   }
 }
 
+template <bool EXACT, bool TAIL, bool OUT_F32>
 __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
   const int per_tile = a.batch * a.q_heads;
   const int t = a.blocks - 1 - (int)(blockIdx.x / per_tile);  // heaviest tiles first
@@ -95,7 +229,15 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
   __shared__ __align__(16) uint16_t vbuf[2][kSubElems];
   __shared__ int list[kA2MaxBlocks];
   __shared__ int list_len;
+  __shared__ uint32_t listed[TAIL ? kA2MaxBlocks / 32 : 1];   // membership of the tile's list
+  __shared__ int16_t tlist[TAIL ? kA2MaxBlocks : 1];          // unlisted history blocks
+  __shared__ float tail_bias[kSub];
+  __shared__ int tail_len;
 
+  if (TAIL) {
+    if (tid < kA2MaxBlocks / 32) listed[tid] = 0u;
+    block_sync();
+  }
   // compacted block list: ids in [0, NB), list order
   if (w == 0) {
     int n = a.idx ? a.cnt[b * a.cs_b + t * a.cs_t + h * a.cs_h] : t + 1;
@@ -108,13 +250,16 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
       const bool ok = j >= 0 && j < a.blocks;
       const uint64_t m = __ballot(ok);
       const int pos = base + __popcll(m & ((1ull << lane) - 1ull));
-      if (ok) list[pos] = (int)j;
+      if (ok) {
+        list[pos] = (int)j;
+        if (TAIL) atomicOr(&listed[j >> 5], 1u << (j & 31));
+      }
       base += __popcll(m);
     }
     if (lane == 0) list_len = base;
   }
   block_sync();
-  const int steps = list_len * 4;
+  const int steps = EXACT ? list_len * 4 : 0;
   const int64_t kv_block0 = ((int64_t)b * a.kv_heads + g) * a.blocks;
 
   auto issue = [&](int s, int buf) {
@@ -143,8 +288,6 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
   // K operand: row col, 16-byte chunk 2 dc + half at ((2 dc + half) ^ (col & 15)):
   // (dc >> 3) * 128 + (e0 ^ ((dc & 7) << 4)) elements past the row start.
   const int e0 = (((col >> 1) & 7) << 4) + ((half ^ (col & 1)) << 3);
-  // V^T operand: dim row 32 dt + col, chunk 2 ks + half at ((2 ks + half) ^ ((col >> 2) & 3))
-  const int vsw = (col >> 2) & 3;
 
   f32x16 o[8];
 #pragma unroll
@@ -159,27 +302,8 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
     if (s + 1 < steps) issue(s + 1, (s + 1) & 1);
     const int j = __builtin_amdgcn_readfirstlane(list[s >> 2]);
     const int sb = s & 3;
-    const uint16_t* kb = kbuf[s & 1] + col * kD2;
-    const uint16_t* vb = vbuf[s & 1];
-
-    // operand reads in groups of four k-steps (fenced), so that at most four K
-    // operands are live: with O (128) and Q (64) the wave stays under 256 VGPRs
-    // and O never leaves the registers it accumulates in
     f32x16 sc = {};
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      bf16x8 kr[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int dc = g4 * 4 + i;
-        kr[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(kb + (dc >> 3) * 128 +
-                                                            (e0 ^ ((dc & 7) << 4))));
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc = mfma32(kr[i], qb[g4 * 4 + i], sc);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-
+    key_products(kbuf[s & 1] + col * kD2, e0, qb, sc);
     // x = s * scale - m (diagonal block: keys above the query at -inf); the lazy
     // max check runs on x, per lane half, and forms the column max over both
     // halves only in the rare branch where some lane exceeds its threshold
@@ -191,76 +315,117 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
       for (int r = 0; r < 16; ++r)
         if (sb * kSub + mfma32_row(r, lane) > qr) x[r] = -INFINITY;
     }
-    float mx = fmaxf(fmaxf(x[0], x[1]), x[2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, x[r]), x[r + 1]);
-    mx = fmaxf(mx, x[15]);
-    if (__any(mx > thr)) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
-                                                       false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      const bool move = mx > thr;
-      const float d = move ? mx : 0.0f;
-      // nothing is accumulated before the first move (thr -inf): O and l stay 0
-      const float corr = thr == -INFINITY ? 0.0f : exp2_fast(-d);
-      // in place (tied operands): O keeps its registers across the rare branch. The
-      // compiler's hazard recognizer does not look inside asm statements, so the
-      // wait states after the last product into O (19 >= the XDL write -> VALU
-      // requirement) are issued first, tied to O.
-      asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 2"
-                   : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(o[4]), "+v"(o[5]),
-                     "+v"(o[6]), "+v"(o[7]));
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(o[dt][r]) : "v"(corr));
-      l *= corr;
-      neg_m -= d;
-      if (move) thr = kLazy;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) x[r] -= d;
-    }
-    // probabilities as bf16 B operands; the running sum adds the rounded values
-    u32x4 pb0, pb1;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      pb0[e] = pack_bf16x2(exp2_fast(x[2 * e]), exp2_fast(x[2 * e + 1]));
-      l = add_bf16_pair(l, pb0[e]);
-      pb1[e] = pack_bf16x2(exp2_fast(x[8 + 2 * e]), exp2_fast(x[8 + 2 * e + 1]));
-      l = add_bf16_pair(l, pb1[e]);
-    }
-#pragma unroll
-    for (int d2 = 0; d2 < 4; ++d2) {
-      bf16x8 vr[4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const uint16_t* vrow = vb + ((2 * d2 + i) * 32 + col) * kSub;
-        vr[2 * i] = as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + ((half ^ vsw) << 3)));
-        vr[2 * i + 1] =
-            as_bf16x8(*reinterpret_cast<const u32x4*>(vrow + (((2 + half) ^ vsw) << 3)));
+    softmax_pv(x, vbuf[s & 1], o, neg_m, thr, l);
+  }
+
+  if constexpr (TAIL) {
+    // the tail: history blocks j < t the tile does not list, ascending
+    if (w == 0) {
+      int base = 0;
+      for (int j0 = 0; j0 < t; j0 += 64) {
+        const int j = j0 + lane;
+        const bool in = j < t && !((listed[j >> 5] >> (j & 31)) & 1u);
+        const uint64_t m = __ballot(in);
+        if (in) tlist[base + __popcll(m & ((1ull << lane) - 1ull))] = (int16_t)j;
+        base += __popcll(m);
       }
+      if (lane == 0) tail_len = base;
+    }
+    block_sync();  // also: every wave is done with the exact blocks' buffers
+    const int ntail = tail_len;
+    const int epb = a.tail_kind == 2 ? 2 : 1;  // entries per unlisted block
+    const int per_sub = kSub / epb;
+    for (int t0 = 0; t0 < ntail; t0 += per_sub) {
+      if (t0 > 0) block_sync();  // every wave is done with the previous tail sub-block
+      // one work item per (entry, 8-dim chunk): 32 x 32 over the four waves
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        o[2 * d2 + i] = mfma32(vr[2 * i], as_bf16x8(pb0), o[2 * d2 + i]);
-        o[2 * d2 + i] = mfma32(vr[2 * i + 1], as_bf16x8(pb1), o[2 * d2 + i]);
+      for (int k4 = 0; k4 < (kSub * (kD2 / 8)) / kA2Threads; ++k4) {
+        const int e = tid + k4 * kA2Threads;
+        const int i = e >> 5, c = e & 31;
+        const int blk = t0 + i / epb, kind = i % epb;
+        const int j = blk < ntail ? (int)tlist[blk] : -1;
+        float mk[8] = {}, mv[8] = {};
+        float bi = -INFINITY;
+        if (j >= 0) {
+          const int64_t off = (((int64_t)b * a.blocks + j) * a.kv_heads + g) * kD2 + c * 8;
+          if (a.tail_kind == 0) {
+            load8f(a.mean_k + off, mk);
+            load8f(a.mean_v + off, mv);
+            bi = logf((float)a.bcounts[j]) * kLog2e;
+          } else {
+            // history blocks j < t are full, so the token is inside the sequence
+            const int tok = a.choice[(((int64_t)b * a.blocks + t) * a.blocks + j) * a.q_heads + h];
+            const u32x4 kraw = *reinterpret_cast<const u32x4*>(
+                a.kt + ((kv_block0 + j) * kBlock + tok) * kD2 + key_chunk_pos(tok, c) * 8);
+            const u32x4 vraw = *reinterpret_cast<const u32x4*>(
+                a.v + b * a.vs_b + ((int64_t)j * kBlock + tok) * a.vs_s + g * a.vs_h + c * 8);
+            float kval[8], vval[8];
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+              kval[2 * x] = bf16_lo(kraw[x]);
+              kval[2 * x + 1] = bf16_hi(kraw[x]);
+              vval[2 * x] = bf16_lo(vraw[x]);
+              vval[2 * x + 1] = bf16_hi(vraw[x]);
+            }
+            if (kind == 0) {
+#pragma unroll
+              for (int x = 0; x < 8; ++x) { mk[x] = kval[x]; mv[x] = vval[x]; }
+              bi = 0.0f;
+            } else {
+              float mean_k[8], mean_v[8];
+              load8f(a.mean_k + off, mean_k);
+              load8f(a.mean_v + off, mean_v);
+#pragma unroll
+              for (int x = 0; x < 8; ++x) {
+                mk[x] = (mean_k[x] * (float)kBlock - kval[x]) / (float)(kBlock - 1);
+                mv[x] = (mean_v[x] * (float)kBlock - vval[x]) / (float)(kBlock - 1);
+              }
+              bi = logf((float)(kBlock - 1)) * kLog2e;
+            }
+          }
+        }
+        write_tail_entry256(kbuf[0], kbuf[1], vbuf[0], i, c, mk, mv);
+        if (c == 0) tail_bias[i] = bi;
       }
-      __builtin_amdgcn_sched_barrier(0);
+      block_sync();
+      f32x16 sc = {};
+      key_products(kbuf[0] + col * kD2, e0, qb, sc);   // hi rows
+      key_products(kbuf[1] + col * kD2, e0, qb, sc);   // lo rows
+      f32x16 x;
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        x[r] = fmaf(sc[r], a.scale_log2, tail_bias[mfma32_row(r, lane)]) + neg_m;
+      softmax_pv(x, vbuf[0], o, neg_m, thr, l);
     }
   }
 
   l += __shfl_xor(l, 32);
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   if (row_ok) {
-    uint16_t* dst = a.out + b * a.os_b + qrow * a.os_s + h * a.os_h + 4 * half;
+    if (OUT_F32) {
+      float* dst = static_cast<float*>(a.out) + b * a.os_b + qrow * a.os_s + h * a.os_h + 4 * half;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
+      for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
-      for (int grp = 0; grp < 4; ++grp) {
-        const int r = 4 * grp;
-        u32x2 v;
-        v[0] = pack_bf16x2(o[dt][r] * inv, o[dt][r + 1] * inv);
-        v[1] = pack_bf16x2(o[dt][r + 2] * inv, o[dt][r + 3] * inv);
-        *reinterpret_cast<u32x2*>(dst + dt * 32 + 8 * grp) = v;
+        for (int grp = 0; grp < 4; ++grp) {
+          const int r = 4 * grp;
+          *reinterpret_cast<f32x4*>(dst + dt * 32 + 8 * grp) =
+              f32x4{o[dt][r] * inv, o[dt][r + 1] * inv, o[dt][r + 2] * inv, o[dt][r + 3] * inv};
+        }
+      }
+    } else {
+      uint16_t* dst =
+          static_cast<uint16_t*>(a.out) + b * a.os_b + qrow * a.os_s + h * a.os_h + 4 * half;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+          const int r = 4 * grp;
+          u32x2 v;
+          v[0] = pack_bf16x2(o[dt][r] * inv, o[dt][r + 1] * inv);
+          v[1] = pack_bf16x2(o[dt][r + 2] * inv, o[dt][r + 3] * inv);
+          *reinterpret_cast<u32x2*>(dst + dt * 32 + 8 * grp) = v;
+        }
       }
     }
     if (a.lse && half == 0)
@@ -269,8 +434,8 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
   }
 }
 
-int launch_attention_256(const void* q, const int64_t* q_strides, const void* key_tiles,
-                         const void* value_tiles, const int64_t* indices,
+int launch_attention_256(const Attn256Options& opt, const void* q, const int64_t* q_strides,
+                         const void* key_tiles, const void* value_tiles, const int64_t* indices,
                          const int64_t* index_strides, const int32_t* counts,
                          const int64_t* count_strides, int batch, int seq, int q_heads,
                          int kv_heads, float scale, void* out, const int64_t* out_strides,
@@ -292,12 +457,24 @@ int launch_attention_256(const void* q, const int64_t* q_strides, const void* ke
   }
   a.batch = batch; a.seq = seq; a.q_heads = q_heads; a.kv_heads = kv_heads; a.blocks = blocks;
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
-  a.out = static_cast<uint16_t*>(out);
+  a.out = out;
   a.os_b = out_strides[0]; a.os_s = out_strides[1]; a.os_h = out_strides[2];
   a.lse = lse;
   if (lse) { a.ls_b = lse_strides[0]; a.ls_s = lse_strides[1]; a.ls_h = lse_strides[2]; }
+  if (opt.tail) {
+    a.tail_kind = opt.tail_kind;
+    a.mean_k = opt.mean_k; a.mean_v = opt.mean_v; a.bcounts = opt.block_counts;
+    a.choice = opt.choice;
+    if (opt.tail_kind > 0) {
+      a.v = static_cast<const uint16_t*>(opt.v);
+      a.vs_b = opt.v_strides[0]; a.vs_s = opt.v_strides[1]; a.vs_h = opt.v_strides[2];
+    }
+  }
   const unsigned grid = (unsigned)(blocks * batch * q_heads);
-  attn256_kernel<<<grid, kA2Threads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (opt.exact && !opt.tail) attn256_kernel<true, false, false><<<grid, kA2Threads, 0, st>>>(a);
+  else if (opt.exact) attn256_kernel<true, true, false><<<grid, kA2Threads, 0, st>>>(a);
+  else attn256_kernel<false, true, true><<<grid, kA2Threads, 0, st>>>(a);
   return launch_status("attention_d256");
 }
 

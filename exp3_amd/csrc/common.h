@@ -117,10 +117,23 @@ __host__ __device__ __forceinline__ int value_slot_of_key(int key) {
 namespace spx {
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);
-// Exact attention at head_dim 256 (attn256.hip); arguments as spx_exact_attention,
-// already validated by the caller.
-int launch_attention_256(const void* q, const int64_t* q_strides, const void* key_tiles,
-                         const void* value_tiles, const int64_t* indices,
+// What a d = 256 attention launch computes besides / instead of the exact blocks
+// (the tails mirror the d = 128 kernel's: block means, or rescue tokens with an
+// optional remainder entry), and whether the output is fp32.
+struct Attn256Options {
+  bool exact, tail, out_f32;
+  int tail_kind;               // 0 block means, 1 rescue token, 2 rescue token + remainder
+  const float* mean_k;         // [B, NB, Hkv, 256] fp32 (tail_kind 0 and 2)
+  const float* mean_v;
+  const int32_t* block_counts; // [NB] (tail_kind 0)
+  const uint8_t* choice;       // [B, NB, NB, Hq] rescue token per (tile, block, head)
+  const void* v;               // V rows of the rescue tokens, strided [B, S, Hkv, 256]
+  const int64_t* v_strides;
+};
+// Attention at head_dim 256 (attn256.hip); arguments as spx_exact_attention and the
+// tail entry points, already validated by the caller.
+int launch_attention_256(const Attn256Options& opt, const void* q, const int64_t* q_strides,
+                         const void* key_tiles, const void* value_tiles, const int64_t* indices,
                          const int64_t* index_strides, const int32_t* counts,
                          const int64_t* count_strides, int batch, int seq, int q_heads,
                          int kv_heads, float scale, void* out, const int64_t* out_strides,
