@@ -26,12 +26,13 @@ struct MeanQArgs {
   int seq, q_heads, blocks;
 };
 
+template <int D>
 __global__ __launch_bounds__(256) void tile_mean_kernel(MeanQArgs a) {
   const int t = blockIdx.x;
   const int b = blockIdx.z;
   const int idx = blockIdx.y * 256 + threadIdx.x;
-  if (idx >= a.q_heads * (kHeadDim / 2)) return;
-  const int h = idx / (kHeadDim / 2), d2 = idx % (kHeadDim / 2);
+  if (idx >= a.q_heads * (D / 2)) return;
+  const int h = idx / (D / 2), d2 = idx % (D / 2);
   const int row0 = t * kBlock;
   const int n = min(kBlock, a.seq - row0);
   const uint16_t* src = a.q + b * a.qs_b + (int64_t)row0 * a.qs_s + h * a.qs_h + 2 * d2;
@@ -42,7 +43,7 @@ __global__ __launch_bounds__(256) void tile_mean_kernel(MeanQArgs a) {
     s1 += bf16_hi(w);
   }
   const float count = (float)n;
-  float* dst = a.qmean + (((int64_t)b * a.blocks + t) * a.q_heads + h) * kHeadDim + 2 * d2;
+  float* dst = a.qmean + (((int64_t)b * a.blocks + t) * a.q_heads + h) * D + 2 * d2;
   dst[0] = s0 / count;
   dst[1] = s1 / count;
 }
@@ -62,14 +63,15 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(const float (&x)[8]) {
 }
 
 // One workgroup per (key block j, kv group g, batch b). The key tile of block j
-// (pool layout: row = token, 16-byte chunk c of row r at c ^ (r & 15)) is staged in
-// LDS once; its 128 token rows are the MFMA A operand (four 32-row tiles). The
+// (pool layout: row = token, 16-byte chunk c of row r at c ^ (r & 15) for c < 16;
+// at D = 256, chunk c < 32 at (c & 16) | ((c & 15) ^ (r & 15))) is staged in LDS once; its 128 token rows are the MFMA A operand (four 32-row tiles). The
 // columns are the (later tile t, q head) pairs of the group, 32 per wave step; their
 // fp32 mean queries are split exactly into three bf16 parts (hi + mid + lo), so
 // three bf16 products per k-step give the fp32 dot products to ~2^-24 relative.
 // Each lane then owns one column's 128 token scores (64 per lane half, in token
 // order): a strict in-lane max keeps the first position, and the two halves merge
 // with the lower position on equal scores (torch.argmax: first maximum).
+template <int D>
 __global__ __launch_bounds__(kChoiceThreads) void rescue_choice_kernel(ChoiceArgs a) {
   const int j = blockIdx.x;
   const int g = blockIdx.y;
@@ -84,30 +86,30 @@ __global__ __launch_bounds__(kChoiceThreads) void rescue_choice_kernel(ChoiceArg
   }
   if (j >= a.blocks - 1) return;  // no later tile
 
-  __shared__ __align__(16) uint16_t kt[kBlock * kHeadDim];  // 32 KB
+  __shared__ __align__(16) uint16_t kt[kBlock * D];  // 32 KB (64 KB at D = 256)
   {
     const u32x4* src = reinterpret_cast<const u32x4*>(
-        a.kt + (((int64_t)b * a.kv_heads + g) * a.blocks + j) * kBlock * kHeadDim);
+        a.kt + (((int64_t)b * a.kv_heads + g) * a.blocks + j) * kBlock * D);
     u32x4* dst = reinterpret_cast<u32x4*>(kt);
-    for (int i = tid; i < kBlock * kHeadDim / 8; i += kChoiceThreads) dst[i] = src[i];
+    for (int i = tid; i < kBlock * D / 8; i += kChoiceThreads) dst[i] = src[i];
   }
   block_sync();
 
   const int ncols = a.group * (a.blocks - 1 - j);
   const int ngroups = (ncols + 31) / 32;
   // LDS element offset of token row (32 rt + col), chunk 2 dc + half:
-  // ((2 dc + half) ^ (col & 15)) << 3 = base ^ (dc << 4), plus rt * 32 rows
-  const int e0 = col * kHeadDim + (((col >> 1) & 7) << 4) + ((half ^ (col & 1)) << 3);
+  // (dc >> 3) * 128 + (base ^ ((dc & 7) << 4)), plus rt * 32 rows
+  const int e0 = (((col >> 1) & 7) << 4) + ((half ^ (col & 1)) << 3);
   for (int grp = w; grp < ngroups; grp += kChoiceThreads / 64) {
     const int c = grp * 32 + col;
     const bool cok = c < ncols;
     const int t = j + 1 + (cok ? c / a.group : 0);
     const int hh = cok ? c % a.group : 0;
-    const float* qm = a.qmean + (((int64_t)b * a.blocks + t) * a.q_heads + g * a.group + hh) * kHeadDim +
+    const float* qm = a.qmean + (((int64_t)b * a.blocks + t) * a.q_heads + g * a.group + hh) * D +
                       half * 8;
     f32x16 acc[4] = {};
 #pragma unroll
-    for (int dc = 0; dc < 8; ++dc) {
+    for (int dc = 0; dc < D / 16; ++dc) {
       float x[8] = {};
       if (cok) {
         const f32x4 x0 = *reinterpret_cast<const f32x4*>(qm + dc * 16);
@@ -123,10 +125,10 @@ __global__ __launch_bounds__(kChoiceThreads) void rescue_choice_kernel(ChoiceArg
 #pragma unroll
       for (int e = 0; e < 8; ++e) r2[e] = r1[e] - (float)mid[e];
       const bf16x8 lo = pack_bf16x8(r2);
-      const int off = e0 ^ (dc << 4);
+      const int off = col * D + (dc >> 3) * 128 + (e0 ^ ((dc & 7) << 4));
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) {
-        const bf16x8 kr = as_bf16x8(*reinterpret_cast<const u32x4*>(kt + rt * 32 * kHeadDim + off));
+        const bf16x8 kr = as_bf16x8(*reinterpret_cast<const u32x4*>(kt + rt * 32 * D + off));
         acc[rt] = mfma32(kr, hi, acc[rt]);
         acc[rt] = mfma32(kr, mid, acc[rt]);
         acc[rt] = mfma32(kr, lo, acc[rt]);
@@ -161,7 +163,8 @@ using namespace spx;
 extern "C" int spx_tile_mean_query(const void* q, const int64_t* q_strides, int batch, int seq,
                                    int q_heads, int head_dim, int block_size, float* qmean,
                                    void* stream) {
-  SPX_REQUIRE(head_dim == kHeadDim, SPX_EUNSUPPORTED, "head_dim %d unsupported (only 128)", head_dim);
+  SPX_REQUIRE(head_dim == kHeadDim || head_dim == 256, SPX_EUNSUPPORTED,
+              "head_dim %d unsupported (128 or 256)", head_dim);
   SPX_REQUIRE(block_size == kBlock, SPX_EUNSUPPORTED, "block_size %d unsupported (only 128)",
               block_size);
   SPX_REQUIRE(batch > 0 && seq > 0 && q_heads > 0, SPX_EINVAL, "bad shape: batch %d seq %d heads %d",
@@ -176,15 +179,17 @@ extern "C" int spx_tile_mean_query(const void* q, const int64_t* q_strides, int 
   a.qs_b = q_strides[0]; a.qs_s = q_strides[1]; a.qs_h = q_strides[2];
   a.qmean = qmean;
   a.seq = seq; a.q_heads = q_heads; a.blocks = num_blocks(seq);
-  dim3 grid(a.blocks, (q_heads * (kHeadDim / 2) + 255) / 256, batch);
-  tile_mean_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  dim3 grid(a.blocks, (q_heads * (head_dim / 2) + 255) / 256, batch);
+  if (head_dim == 256) tile_mean_kernel<256><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  else tile_mean_kernel<kHeadDim><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   return launch_status("tile_mean_query");
 }
 
 extern "C" int spx_rescue_choice(const float* qmean, const void* key_tiles, int batch, int seq,
                                  int q_heads, int kv_heads, int head_dim, int block_size,
                                  uint8_t* choice, void* stream) {
-  SPX_REQUIRE(head_dim == kHeadDim, SPX_EUNSUPPORTED, "head_dim %d unsupported (only 128)", head_dim);
+  SPX_REQUIRE(head_dim == kHeadDim || head_dim == 256, SPX_EUNSUPPORTED,
+              "head_dim %d unsupported (128 or 256)", head_dim);
   SPX_REQUIRE(block_size == kBlock, SPX_EUNSUPPORTED, "block_size %d unsupported (only 128)",
               block_size);
   SPX_REQUIRE(batch > 0 && seq > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
@@ -202,6 +207,7 @@ extern "C" int spx_rescue_choice(const float* qmean, const void* key_tiles, int 
   a.group = q_heads / kv_heads;
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid(a.blocks, kv_heads, batch);
-  rescue_choice_kernel<<<grid, kChoiceThreads, 0, st>>>(a);
+  if (head_dim == 256) rescue_choice_kernel<256><<<grid, kChoiceThreads, 0, st>>>(a);
+  else rescue_choice_kernel<kHeadDim><<<grid, kChoiceThreads, 0, st>>>(a);
   return launch_status("rescue_choice");
 }

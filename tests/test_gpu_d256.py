@@ -220,7 +220,7 @@ def test_attention_tiles_layout_d256(gpu, length):
 def test_other_methods_raise_at_d256(gpu):
     q, k, v = qkv(257, seed=23)
     backend = attention.AttentionBackend(alpha=0.08, register=False)
-    for method in ("cgf_mean", "fp_v1_rescue"):
+    for method in ("cgf_mean",):
         backend.configure(method, 0.08)
         with pytest.raises(ValueError, match="head_dim"):
             _backend_forward(backend, q.cuda(), k.cuda(), v.cuda())
