@@ -293,10 +293,6 @@ class AttentionBackend:
             k = _lib.kernel_view(key.transpose(1, 2))
             v = _lib.kernel_view(value.transpose(1, 2))
             scale = float(scaling)
-            if q.shape[-1] != 128 and self.method not in V1_ROUTED_METHODS:
-                raise ValueError(
-                    f"{self.method} needs head_dim 128 (got {q.shape[-1]}); at head_dim 256 "
-                    "the HIP path runs dense and the V1-routed methods")
             capture_v1 = self.capture_callback is not None and self.method == "fp_v1"
             if self.method in V1_ROUTED_METHODS:
                 kbar, descriptors, tiles, scores, indices, counts, selected = self._route_v1(

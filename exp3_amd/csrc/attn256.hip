@@ -74,6 +74,13 @@ struct Attn256Args {
   int64_t vs_b, vs_s, vs_h;
 };
 
+// Keep `x` opaque inside a loop so values derived from it are recomputed per use
+// instead of being hoisted (and held in registers) as loop invariants.
+__device__ __forceinline__ int opaque256(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // Position of 16-byte chunk c (< 32) of K row r in the d = 256 key layout.
 __device__ __forceinline__ int key_chunk_pos(int r, int c) { return (c & 16) | ((c & 15) ^ (r & 15)); }
 
@@ -337,10 +344,12 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
     const int per_sub = kSub / epb;
     for (int t0 = 0; t0 < ntail; t0 += per_sub) {
       if (t0 > 0) block_sync();  // every wave is done with the previous tail sub-block
-      // one work item per (entry, 8-dim chunk): 32 x 32 over the four waves
-#pragma unroll
+      // one work item per (entry, 8-dim chunk): 32 x 32 over the four waves. Not
+      // unrolled: with O (128) and Q (64) live, four items' temporaries at once
+      // would push the wave past 256 registers (AGPR spills, one wave per SIMD)
+#pragma unroll 1
       for (int k4 = 0; k4 < (kSub * (kD2 / 8)) / kA2Threads; ++k4) {
-        const int e = tid + k4 * kA2Threads;
+        const int e = opaque256(tid) + k4 * kA2Threads;
         const int i = e >> 5, c = e & 31;
         const int blk = t0 + i / epb, kind = i % epb;
         const int j = blk < ntail ? (int)tlist[blk] : -1;
@@ -388,13 +397,16 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
         if (c == 0) tail_bias[i] = bi;
       }
       block_sync();
+      const int lane_t = opaque256(lane);
+      const int col_t = lane_t & 31;
+      const int e0_t = (((col_t >> 1) & 7) << 4) + (((lane_t >> 5) ^ (col_t & 1)) << 3);
       f32x16 sc = {};
-      key_products(kbuf[0] + col * kD2, e0, qb, sc);   // hi rows
-      key_products(kbuf[1] + col * kD2, e0, qb, sc);   // lo rows
+      key_products(kbuf[0] + col_t * kD2, e0_t, qb, sc);   // hi rows
+      key_products(kbuf[1] + col_t * kD2, e0_t, qb, sc);   // lo rows
       f32x16 x;
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        x[r] = fmaf(sc[r], a.scale_log2, tail_bias[mfma32_row(r, lane)]) + neg_m;
+        x[r] = fmaf(sc[r], a.scale_log2, tail_bias[mfma32_row(r, lane_t)]) + neg_m;
       softmax_pv(x, vbuf[0], o, neg_m, thr, l);
     }
   }

@@ -14,14 +14,16 @@
 //       q.mu   = q.mu_hi + q.mu_lo                          (2 MFMA)
 //       q2.var = q2_hi.var_hi + q2_hi.var_lo + q2_lo.var_hi (3 MFMA, drops 2^-16 term)
 //   * selector_split_kernel splits mu_K and var_K once per call into a workspace
-//     whose 32-block chunks are the LDS image the score kernel wants: per chunk,
-//     parts [mu hi, mu lo, var hi, var lo] x 32 block rows x 128 dims bf16, 16-byte
-//     chunk c of row r at position c ^ (r & 15) (bank-conflict-free operand reads).
+//     whose 32-block chunks are the LDS image the score kernel wants: per chunk and
+//     128-dim half (one half at D = 128, two at D = 256), parts [mu hi, mu lo,
+//     var hi, var lo] x 32 block rows x 128 dims bf16, 16-byte chunk c of row r at
+//     position c ^ (r & 15) (bank-conflict-free operand reads).
 //   * selector_kernel: one workgroup per (tile, q head), four waves of 32 query
-//     rows holding Q (and the q*q hi/lo split) in registers as MFMA B operands.
-//     The workspace chunks stream through two LDS buffers with direct global->LDS
-//     loads (chunk s + 1 lands while chunk s is computed; one barrier per chunk)
-//     and serve all four waves. Scores are formed transposed (block j = MFMA row,
+//     rows holding Q (and, at D = 128, the q*q hi/lo split) in registers as MFMA B
+//     operands; at D = 256 the split is formed from Q per k-step. The workspace
+//     half-chunks stream through two LDS buffers with direct global->LDS loads
+//     (step s + 1 lands while step s is computed; one barrier per step) and serve
+//     all four waves; a chunk's logits are formed after its last half. Scores are formed transposed (block j = MFMA row,
 //     query = lane column), so the per-row softmax is an in-lane online reduction
 //     plus one lane-half exchange; the second pass recomputes the logits, and the
 //     per-block sum over the tile's rows is a 16-shuffle transpose-reduction across
@@ -35,14 +37,14 @@ namespace spx {
 constexpr int kSelThreads = 256;
 constexpr int kSelMaxBlocks = 1024;
 constexpr int kSelChunk = 32;                          // blocks per chunk
-constexpr int kSelPart = kSelChunk * kHeadDim;         // bf16 elements of one part
-constexpr int kSelChunkElems = 4 * kSelPart;           // 32 KB
+constexpr int kSelPart = kSelChunk * 128;             // bf16 elements of one part (128-dim half)
+constexpr int kSelChunkElems = 4 * kSelPart;           // 32 KB per 128-dim half of a chunk
 
 struct SplitArgs {
   const float* mean_k;  // [B, NB, Hkv, D]
   const float* var_k;
-  uint16_t* ws;         // [B, Hkv, NC, 4, 32, D] bf16
-  int batch, kv_heads, blocks, chunks;
+  uint16_t* ws;         // [B, Hkv, NC, D / 128, 4, 32, 128] bf16
+  int batch, kv_heads, blocks, chunks, dim;
   bool second_order;
 };
 
@@ -58,17 +60,18 @@ __device__ __forceinline__ void split8(const float* v, u32x4& hi, u32x4& lo) {
 // One thread per (b, g, block j of the padded range, 8-dim chunk c).
 __global__ __launch_bounds__(256) void selector_split_kernel(SplitArgs a) {
   const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t total = (int64_t)a.batch * a.kv_heads * a.chunks * kSelChunk * 16;
+  const int cpr = a.dim / 8;   // 8-dim chunks per row
+  const int64_t total = (int64_t)a.batch * a.kv_heads * a.chunks * kSelChunk * cpr;
   if (id >= total) return;
-  const int c = (int)(id & 15);
-  const int64_t rest = id >> 4;
+  const int c = (int)(id % cpr);
+  const int64_t rest = id / cpr;
   const int jp = (int)(rest % ((int64_t)a.chunks * kSelChunk));
   const int64_t bg = rest / ((int64_t)a.chunks * kSelChunk);
   const int g = (int)(bg % a.kv_heads), b = (int)(bg / a.kv_heads);
   const int row = jp % kSelChunk, jc = jp / kSelChunk;
   float mu[8] = {}, var[8] = {};
   if (jp < a.blocks) {
-    const int64_t off = (((int64_t)b * a.blocks + jp) * a.kv_heads + g) * kHeadDim + c * 8;
+    const int64_t off = (((int64_t)b * a.blocks + jp) * a.kv_heads + g) * a.dim + c * 8;
     const f32x4 m0 = *reinterpret_cast<const f32x4*>(a.mean_k + off);
     const f32x4 m1 = *reinterpret_cast<const f32x4*>(a.mean_k + off + 4);
 #pragma unroll
@@ -80,8 +83,9 @@ __global__ __launch_bounds__(256) void selector_split_kernel(SplitArgs a) {
       for (int x = 0; x < 4; ++x) { var[x] = v0[x]; var[4 + x] = v1[x]; }
     }
   }
-  uint16_t* dst = a.ws + ((bg * a.chunks + jc) * kSelChunkElems) + row * kHeadDim +
-                  ((c ^ (row & 15)) << 3);
+  const int halves = a.dim / 128, hf = c >> 4, c16 = c & 15;
+  uint16_t* dst = a.ws + (((bg * a.chunks + jc) * halves + hf) * kSelChunkElems) + row * 128 +
+                  ((c16 ^ (row & 15)) << 3);
   u32x4 hi, lo;
   split8(mu, hi, lo);
   *reinterpret_cast<u32x4*>(dst) = hi;
@@ -164,11 +168,59 @@ __device__ __forceinline__ void dma_chunk(const uint16_t* src, uint16_t* lds, in
   }
 }
 
-template <int SEL>
+// mu and var products of one 128-dim half (Q dims 128 HF ..) against the chunk
+// image in LDS, accumulated into dmu / dvar. At D = 128 the q*q split comes from
+// registers; at D = 256 it is formed from Q here (q*q is exact in fp32).
+template <bool kSecond, int D, int HF>
+__device__ __forceinline__ void selector_products(const uint16_t* ops, int e0,
+                                                  const bf16x8 (&qb)[D / 16],
+                                                  const bf16x8 (&q2h)[8], const bf16x8 (&q2l)[8],
+                                                  f32x16& dmu, f32x16& dvar) {
+#pragma unroll
+  for (int dc = 0; dc < 8; ++dc) {
+    const int off = e0 ^ (dc << 4);
+    const bf16x8 q = qb[HF * 8 + dc];
+    const bf16x8 mh = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + off));
+    const bf16x8 ml = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + kSelPart + off));
+    dmu = mfma32(mh, q, dmu);
+    dmu = mfma32(ml, q, dmu);
+    if (kSecond) {
+      bf16x8 sh, sl;
+      if (D == 128) {
+        sh = q2h[dc];
+        sl = q2l[dc];
+      } else {
+        // opaque copy: the split is formed here for every use instead of being
+        // hoisted out of the chunk loop (which would hold 128 more registers)
+        u32x4 raw = __builtin_bit_cast(u32x4, q);
+        asm volatile("" : "+v"(raw));
+        float sq[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = bf16_lo(raw[e]), x1 = bf16_hi(raw[e]);
+          sq[2 * e] = x0 * x0;
+          sq[2 * e + 1] = x1 * x1;
+        }
+        u32x4 hi, lo;
+        split8(sq, hi, lo);
+        sh = as_bf16x8(hi);
+        sl = as_bf16x8(lo);
+      }
+      const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + 2 * kSelPart + off));
+      const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + 3 * kSelPart + off));
+      dvar = mfma32(vh, sh, dvar);
+      dvar = mfma32(vl, sh, dvar);
+      dvar = mfma32(vh, sl, dvar);
+    }
+  }
+}
+
+template <int SEL, int D>
 __global__ __launch_bounds__(kSelThreads, 2) void selector_kernel(SelArgs a) {
   constexpr bool kSecond = SEL != SPX_SELECTOR_MEAN_BALANCED;
   constexpr bool kDisp = SEL == SPX_SELECTOR_DISPERSION_MEAN;
   constexpr int kParts = kSecond ? 4 : 2;
+  constexpr int kHalves = D / 128;
   const int per_tile = a.batch * a.q_heads;
   const int t = a.blocks - 1 - blockIdx.x / per_tile;  // heaviest tiles first
   const int bh = blockIdx.x % per_tile;
@@ -185,7 +237,9 @@ __global__ __launch_bounds__(kSelThreads, 2) void selector_kernel(SelArgs a) {
   __shared__ float tile_score[kSelMaxBlocks];
 
   const int nchunks = (t + kSelChunk - 1) / kSelChunk;  // visible blocks j < t
-  const uint16_t* src = a.ws + ((int64_t)b * a.kv_heads + g) * a.chunks * kSelChunkElems;
+  const int pass_steps = nchunks * kHalves;              // (chunk, half) steps per pass
+  const uint16_t* src =
+      a.ws + ((int64_t)b * a.kv_heads + g) * a.chunks * kHalves * kSelChunkElems;
   if (nchunks > 0) dma_chunk<kParts>(src, buf[0], tid);
 
   for (int j = tid; j < t; j += kSelThreads) {
@@ -196,15 +250,15 @@ __global__ __launch_bounds__(kSelThreads, 2) void selector_kernel(SelArgs a) {
   const int64_t qrow = (int64_t)t * kBlock + w * 32 + col;
   const bool row_ok = qrow < a.seq;
   const int tile_rows = min(kBlock, a.seq - t * kBlock);
-  bf16x8 qb[8], q2h[8], q2l[8];
+  bf16x8 qb[D / 16], q2h[8], q2l[8];
   {
     const uint16_t* qsrc = a.q + b * a.qs_b + qrow * a.qs_s + h * a.qs_h + half * 8;
 #pragma unroll
-    for (int dc = 0; dc < 8; ++dc) {
+    for (int dc = 0; dc < D / 16; ++dc) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (row_ok) raw = *reinterpret_cast<const u32x4*>(qsrc + dc * 16);
       qb[dc] = as_bf16x8(raw);
-      if (kSecond) {
+      if (kSecond && D == 128) {
         float sq[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -214,8 +268,8 @@ __global__ __launch_bounds__(kSelThreads, 2) void selector_kernel(SelArgs a) {
         }
         u32x4 hi, lo;
         split8(sq, hi, lo);
-        q2h[dc] = as_bf16x8(hi);
-        q2l[dc] = as_bf16x8(lo);
+        q2h[dc & 7] = as_bf16x8(hi);
+        q2l[dc & 7] = as_bf16x8(lo);
       }
     }
   }
@@ -225,26 +279,28 @@ __global__ __launch_bounds__(kSelThreads, 2) void selector_kernel(SelArgs a) {
   const float scale2 = a.scale * a.scale;
   // LDS element offset of this lane's operand row (block col) at 16-byte chunk
   // 2 dc + half: (2 dc + half) ^ (col & 15) = base ^ (dc << 4) in elements.
-  const int e0 = col * kHeadDim + (((col >> 1) & 7) << 4) + ((half ^ (col & 1)) << 3);
+  const int e0 = col * 128 + (((col >> 1) & 7) << 4) + ((half ^ (col & 1)) << 3);
 
   float m_run = -INFINITY, l_run = 0.0f;  // per-row softmax state, log2 units
   float inv_l = 0.0f;
-  const int steps = 2 * nchunks;
+  f32x16 dmu = {}, dvar = {};
+  const int steps = 2 * pass_steps;
   for (int s = 0; s < steps; ++s) {
-    const int jc = s < nchunks ? s : s - nchunks;
-    const bool second_pass = s >= nchunks;
+    const bool second_pass = s >= pass_steps;
+    const int sp = second_pass ? s - pass_steps : s;
+    const int jc = sp / kHalves, hf = sp % kHalves;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    block_sync();  // chunk s landed everywhere; buffer (s + 1) & 1 is free
-    if (second_pass && jc > 0 && tid < kSelChunk) {
+    block_sync();  // step s landed everywhere; buffer (s + 1) & 1 is free
+    if (second_pass && hf == 0 && jc > 0 && tid < kSelChunk) {
       const int j = (jc - 1) * kSelChunk + tid;
       const float(&pp)[4][kSelChunk] = part[(jc - 1) & 1];
       tile_score[j] = pp[0][tid] + pp[1][tid] + pp[2][tid] + pp[3][tid];
     }
     if (s + 1 < steps) {
-      const int nj = s + 1 < nchunks ? s + 1 : s + 1 - nchunks;
-      dma_chunk<kParts>(src + (int64_t)nj * kSelChunkElems, buf[(s + 1) & 1], tid);
+      const int ns = s + 1 < pass_steps ? s + 1 : s + 1 - pass_steps;
+      dma_chunk<kParts>(src + (int64_t)ns * kSelChunkElems, buf[(s + 1) & 1], tid);
     }
-    if (s == nchunks) {
+    if (s == pass_steps) {
       // merge the per-row state of the two lane halves (disjoint block sets)
       const float om = xor32(m_run), ol = xor32(l_run);
       const float nm = fmaxf(m_run, om);
@@ -259,22 +315,14 @@ __global__ __launch_bounds__(kSelThreads, 2) void selector_kernel(SelArgs a) {
     }
 
     const uint16_t* ops = buf[s & 1];
-    f32x16 dmu = {}, dvar = {};
-#pragma unroll
-    for (int dc = 0; dc < 8; ++dc) {
-      const int off = e0 ^ (dc << 4);
-      const bf16x8 mh = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + off));
-      const bf16x8 ml = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + kSelPart + off));
-      dmu = mfma32(mh, qb[dc], dmu);
-      dmu = mfma32(ml, qb[dc], dmu);
-      if (kSecond) {
-        const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + 2 * kSelPart + off));
-        const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + 3 * kSelPart + off));
-        dvar = mfma32(vh, q2h[dc], dvar);
-        dvar = mfma32(vl, q2h[dc], dvar);
-        dvar = mfma32(vh, q2l[dc], dvar);
-      }
+    if (hf == 0) {
+      dmu = f32x16{};
+      dvar = f32x16{};
+      selector_products<kSecond, D, 0>(ops, e0, qb, q2h, q2l, dmu, dvar);
+    } else if constexpr (kHalves > 1) {
+      selector_products<kSecond, D, kHalves - 1>(ops, e0, qb, q2h, q2l, dmu, dvar);
     }
+    if (hf != kHalves - 1) continue;   // the chunk's other half is still to come
 
     // logits in log2 units: (scale q.mu + ln n + u / 2) * log2 e; blocks j >= t
     // (only in the last chunk) are masked. Rows past the sequence end (Q = 0) give
@@ -344,8 +392,8 @@ using namespace spx;
 static int64_t selector_chunks(int seq) { return (num_blocks(seq) + kSelChunk - 1) / kSelChunk; }
 
 extern "C" int64_t spx_selector_workspace_bytes(int batch, int seq, int kv_heads, int head_dim) {
-  if (batch <= 0 || seq <= 0 || kv_heads <= 0 || head_dim != kHeadDim) return -1;
-  return (int64_t)batch * kv_heads * selector_chunks(seq) * kSelChunkElems * 2;
+  if (batch <= 0 || seq <= 0 || kv_heads <= 0 || (head_dim != 128 && head_dim != 256)) return -1;
+  return (int64_t)batch * kv_heads * selector_chunks(seq) * (head_dim / 128) * kSelChunkElems * 2;
 }
 
 namespace {
@@ -358,7 +406,8 @@ int run_selectors(const void* q, const int64_t* q_strides, const float* mean_k,
   SPX_REQUIRE(selector == SPX_SELECTOR_MEAN_BALANCED || selector == SPX_SELECTOR_CGF_MEAN ||
                   selector == SPX_SELECTOR_DISPERSION_MEAN,
               SPX_EINVAL, "unsupported selector id %d", selector);
-  SPX_REQUIRE(head_dim == kHeadDim, SPX_EUNSUPPORTED, "head_dim %d unsupported (only 128)", head_dim);
+  SPX_REQUIRE(head_dim == 128 || head_dim == 256, SPX_EUNSUPPORTED,
+              "head_dim %d unsupported (128 or 256)", head_dim);
   SPX_REQUIRE(block_size == kBlock, SPX_EUNSUPPORTED, "block_size %d unsupported (only 128)", block_size);
   SPX_REQUIRE(batch > 0 && seq > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0,
               SPX_EINVAL, "bad shape");
@@ -381,8 +430,9 @@ int run_selectors(const void* q, const int64_t* q_strides, const float* mean_k,
   sa.mean_k = mean_k; sa.var_k = var_k;
   sa.ws = static_cast<uint16_t*>(workspace);
   sa.batch = batch; sa.kv_heads = kv_heads; sa.blocks = blocks; sa.chunks = chunks;
+  sa.dim = head_dim;
   sa.second_order = selector != SPX_SELECTOR_MEAN_BALANCED;
-  const int64_t threads = (int64_t)batch * kv_heads * chunks * kSelChunk * 16;
+  const int64_t threads = (int64_t)batch * kv_heads * chunks * kSelChunk * (head_dim / 8);
   selector_split_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(sa);
   int rc = launch_status("selector_split");
   if (rc) return rc;
@@ -399,16 +449,30 @@ int run_selectors(const void* q, const int64_t* q_strides, const float* mean_k,
   a.ss_b = score_strides[0]; a.ss_t = score_strides[1]; a.ss_j = score_strides[2];
   a.ss_h = score_strides[3];
   const unsigned grid = (unsigned)(blocks * batch * q_heads);
-  switch (selector) {
-    case SPX_SELECTOR_MEAN_BALANCED:
-      selector_kernel<SPX_SELECTOR_MEAN_BALANCED><<<grid, kSelThreads, 0, st>>>(a);
-      break;
-    case SPX_SELECTOR_CGF_MEAN:
-      selector_kernel<SPX_SELECTOR_CGF_MEAN><<<grid, kSelThreads, 0, st>>>(a);
-      break;
-    default:
-      selector_kernel<SPX_SELECTOR_DISPERSION_MEAN><<<grid, kSelThreads, 0, st>>>(a);
-      break;
+  if (head_dim == 256) {
+    switch (selector) {
+      case SPX_SELECTOR_MEAN_BALANCED:
+        selector_kernel<SPX_SELECTOR_MEAN_BALANCED, 256><<<grid, kSelThreads, 0, st>>>(a);
+        break;
+      case SPX_SELECTOR_CGF_MEAN:
+        selector_kernel<SPX_SELECTOR_CGF_MEAN, 256><<<grid, kSelThreads, 0, st>>>(a);
+        break;
+      default:
+        selector_kernel<SPX_SELECTOR_DISPERSION_MEAN, 256><<<grid, kSelThreads, 0, st>>>(a);
+        break;
+    }
+  } else {
+    switch (selector) {
+      case SPX_SELECTOR_MEAN_BALANCED:
+        selector_kernel<SPX_SELECTOR_MEAN_BALANCED, 128><<<grid, kSelThreads, 0, st>>>(a);
+        break;
+      case SPX_SELECTOR_CGF_MEAN:
+        selector_kernel<SPX_SELECTOR_CGF_MEAN, 128><<<grid, kSelThreads, 0, st>>>(a);
+        break;
+      default:
+        selector_kernel<SPX_SELECTOR_DISPERSION_MEAN, 128><<<grid, kSelThreads, 0, st>>>(a);
+        break;
+    }
   }
   return launch_status("selector_scores");
 }
@@ -436,7 +500,7 @@ extern "C" int spx_selector_scores(const void* q, const int64_t* q_strides, cons
 // every workspace entry a call reads (padded block rows as zeros), so nothing is
 // cleared between calls; calls that overlap on one GPU race on the array.
 
-constexpr int64_t kSelectorScratchBytes = 8ll << 20;   // B * Hkv * ceil(NB / 32) <= 256
+constexpr int64_t kSelectorScratchBytes = 8ll << 20;   // B * Hkv * ceil(NB / 32) * (D / 128) <= 256
 
 static __device__ __align__(256) uint8_t scratch[kSelectorScratchBytes];
 
@@ -487,8 +551,8 @@ extern "C" int spx_selector_scores_noalloc(const void* q, const int64_t* q_strid
               kv_heads, head_dim);
   SPX_REQUIRE(need <= kSelectorScratchBytes, SPX_EUNSUPPORTED,
               "workspace of %lld bytes exceeds the %lld-byte static scratch (batch x kv_heads x "
-              "ceil(blocks / 32) must be at most 256); use spx_selector_scores with a caller "
-              "workspace", (long long)need, (long long)kSelectorScratchBytes);
+              "ceil(blocks / 32) x head_dim / 128 must be at most 256); use spx_selector_scores "
+              "with a caller workspace", (long long)need, (long long)kSelectorScratchBytes);
   void* workspace = nullptr;
   const int rc = scratch_address(stream, &workspace);
   if (rc) return rc;

@@ -97,7 +97,7 @@ def selector_scores(q: torch.Tensor, descriptors: BlockDescriptors, scale: float
     scores = torch.empty(batch, blocks, blocks, q_heads, dtype=torch.float32, device=device)
     nbytes = _lib.load().spx_selector_workspace_bytes(batch, sequence, kv_heads, head_dim)
     if nbytes < 0:
-        raise ValueError(f"selector_scores: unsupported shape {tuple(q.shape)} (head_dim 128 only)")
+        raise ValueError(f"selector_scores: unsupported shape {tuple(q.shape)} (head_dim 128 or 256)")
     workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
     _lib.call("spx_selector_scores", _lib.ptr(q), _lib.strides(q), _lib.ptr(mean_k),
               _lib.ptr(var_k), _lib.ptr(sigma_v), _lib.ptr(counts), batch, sequence, q_heads,

@@ -18,11 +18,9 @@
  *   - Score / mask / index tensors use [batch, query_block, key_block, head].
  *     Outputs documented as "contiguous" must be densely packed in that order.
  *   - bf16 tensors are raw 16-bit bf16 bit patterns; masks are uint8 (0 / 1).
- *   - block_size must be 128 and head_dim 128 (the Qwen2.5-7B routing shape);
- *     spx_block_pool / spx_block_mean_k / spx_block_descriptors, spx_v1_scores /
- *     spx_v1_route and spx_exact_attention also take head_dim 256 (Qwen3.5
- *     full-attention layers, check_qwen35_math.py). q_heads must be a multiple
- *     of kv_heads.
+ *   - block_size must be 128; head_dim 128 (the Qwen2.5-7B shape) or 256 (Qwen3.5
+ *     full-attention layers, check_qwen35_math.py) for every entry point that
+ *     takes one. q_heads must be a multiple of kv_heads.
  *   - Return 0 on success or a negative SPX_E* code; spx_last_error() then
  *     returns a thread-local message.
  */
@@ -156,13 +154,13 @@ int spx_selector_scores(const void* q, const int64_t* q_strides, const float* me
                         int block_size, int selector, float scale, void* workspace,
                         float* score, const int64_t* score_strides, void* stream);
 
-/* Bytes of the spx_selector_scores workspace (B * Hkv * ceil(NB / 32) * 32 KB), or -1
+/* Bytes of the spx_selector_scores workspace (B * Hkv * ceil(NB / 32) * D / 128 * 32 KB), or -1
  * for an unsupported shape. Helper of spx_selector_scores (no reference counterpart). */
 int64_t spx_selector_workspace_bytes(int batch, int seq, int kv_heads, int head_dim);
 
 /* spx_selector_scores without the workspace argument and without any allocation: the
  * split workspace is a file-scope device array of 8 MiB per GPU (held until the
- * process ends), so the shape must satisfy B * Hkv * ceil(NB / 32) <= 256, i.e.
+ * process ends), so the shape must satisfy B * Hkv * ceil(NB / 32) * D / 128 <= 256, i.e.
  * spx_selector_workspace_bytes() <= 8 MiB (larger shapes return SPX_EUNSUPPORTED).
  * Results are identical to spx_selector_scores'. The stream must belong to the
  * current device. Calls that overlap on one GPU race on the shared array.

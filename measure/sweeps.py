@@ -15,9 +15,10 @@
       and rescue tails; mean_native, fp_v1, cgf_mean, fp_v1_rescue_v2 and dense
   python -m measure.sweeps d256 [--seq 32640]
       head_dim 256 with 16 query / 4 KV heads (Qwen3.5 full-attention layer shape,
-      check_qwen35_math.py): dense (torch SDPA and the HIP kernel) and fp_v1 at
-      alpha 0.08; ms/layer, the attention kernel's HIP-event time and its rate over
-      the selected 128 x 128 tiles (4 x 128 x 128 x 256 FLOP each)
+      check_qwen35_math.py): dense (torch SDPA and the HIP kernel) and every sparse
+      method at alpha 0.08, and four methods on Q, K x 4 at alpha 0.7 (sparse
+      lists, non-empty tails); ms/layer, the attention kernel's HIP-event time and
+      its rate over the selected 128 x 128 tiles (4 x 128 x 128 x 256 FLOP each)
   python -m measure.sweeps pair-overlap [--seq 32640] [--qk-scale 4] [--alpha 0.7]
       fp_v1 on sharpened inputs: the attention kernel on the routed lists and on
       lists where each tile pair's lists coincide (tile t - 1 takes tile t's routed
@@ -141,12 +142,20 @@ def run_d256(seq, seed):
     _lib.load()
     q, k, v, _ = synthetic.make_inputs(seq, seed=seed, q_heads=16, kv_heads=4, head_dim=256,
                                        device="cuda")
-    cases = [("dense", "sdpa"), ("dense", "hip"), ("fp_v1", "sdpa")]
-    for method, dense_impl in cases:
-        row = _layer_case(torch, attention, kernels, q, k, v, method, 0.08, steps=5, warmup=2,
+    cases = [("dense", "sdpa", 0.08, 1.0), ("dense", "hip", 0.08, 1.0)]
+    cases += [(m, "sdpa", 0.08, 1.0) for m in attention.METHODS[1:]]
+    # sharpened inputs (Q, K x 4) at alpha 0.7: sparse lists, non-empty tails
+    cases += [(m, "sdpa", 0.7, 4.0) for m in ("fp_v1", "mean_native", "cgf_mean",
+                                             "fp_v1_rescue_v2")]
+    for method, dense_impl, alpha, qk in cases:
+        qq, kk = q, k
+        if qk != 1.0:
+            qq = (q.float() * qk).to(torch.bfloat16)
+            kk = (k.float() * qk).to(torch.bfloat16)
+        row = _layer_case(torch, attention, kernels, qq, kk, v, method, alpha, steps=5, warmup=2,
                           dense_impl=dense_impl, scale=256 ** -0.5)
         row.update({"sweep": "d256", "q_heads": 16, "kv_heads": 4, "head_dim": 256,
-                    "impl": dense_impl if method == "dense" else "hip"})
+                    "qk_scale": qk, "impl": dense_impl if method == "dense" else "hip"})
         print(json.dumps(row), flush=True)
 
 

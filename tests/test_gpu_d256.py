@@ -217,13 +217,16 @@ def test_attention_tiles_layout_d256(gpu, length):
     np.testing.assert_array_equal(sub, want_v)
 
 
-def test_other_methods_raise_at_d256(gpu):
-    q, k, v = qkv(257, seed=23)
+def test_unsupported_head_dim_raises(gpu):
+    """Head dims other than 128 and 256 are refused with ValueError by every path
+    (the kernels' SPX_EUNSUPPORTED), before any launch."""
+    g = torch.Generator().manual_seed(23)
+    q = torch.randn(1, 257, 8, 64, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(1, 257, 2, 64, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(1, 257, 2, 64, generator=g).to(torch.bfloat16).cuda()
     backend = attention.AttentionBackend(alpha=0.08, register=False)
-    for method in ("cgf_mean",):
+    for method in ("fp_v1", "mean_native", "cgf_mean", "fp_v1_rescue"):
         backend.configure(method, 0.08)
         with pytest.raises(ValueError, match="head_dim"):
-            _backend_forward(backend, q.cuda(), k.cuda(), v.cuda())
-    with pytest.raises(ValueError, match="head_dim"):
-        kernels.selector_scores(q.cuda(), kernels.block_descriptors(k.cuda(), v.cuda()), SCALE,
-                                "cgf_mean")
+            backend.forward(_Layer(), q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                            None, 64 ** -0.5)

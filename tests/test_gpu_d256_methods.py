@@ -22,7 +22,7 @@ LENGTH = 2113   # 17 blocks, the last one 65 rows
 ALPHA = 0.7
 Q_HEADS, KV_HEADS, DIM = 16, 4, 256
 SCALE = DIM ** -0.5
-D256_METHODS = ("fp_v1", "mean_native", "fp_v1_rescue", "fp_v1_rescue_v2")
+D256_METHODS = attention.METHODS[1:]   # every method but dense (test_gpu_d256.py)
 
 
 class _Layer:
@@ -48,64 +48,46 @@ def test_methods_d256_vs_oracle(gpu, method):
     assert out.shape == (1, LENGTH, Q_HEADS, DIM)
     blocks = ref.num_blocks(LENGTH)
     assert expected["selected"].sum() < Q_HEADS * blocks * (blocks + 1) // 2   # sparse
+    record = {"events": {}}
     if method in attention.V1_ROUTED_METHODS:
-        record = {"events": {}}
         _, _, _, _, _, _, sel = backend._route_v1(qg, kg, vg, SCALE, record, False, False)
         unexplained, _, _ = masks_equal_except_ties(to_np(sel), expected["selected"],
                                                      threshold_ties(expected["scores"], ALPHA))
         assert unexplained == 0
-        # always compared: the oracle layer given the GPU's own selection (and, for
-        # the rescue methods, the GPU's rescue tokens: fp32 near-ties may pick another)
-        choice = None
-        if method in attention.RESCUE_METHODS:
-            choice = to_np(kernels.rescue_choice(qg, up.attention_tiles(kg, vg)[0]))
-        want, _ = ref.attention_from_selection(to_np(q), to_np(k), to_np(v), SCALE, method,
-                                               to_np(sel), choice=choice)
-        assert_output_close(to_np(out), want, what=f"{method} d256 (GPU lists)", rel=2.0 ** -7)
+    else:
+        _, _, _, _, sel = backend._new_selection(qg, kg, vg, SCALE, record)
+        ties = threshold_ties(expected["scores"], ALPHA, positive_rule=True)
+        unexplained, _, _ = masks_equal_except_ties(to_np(sel), expected["selected"], ties)
+        assert unexplained == 0
+    # always compared: the oracle layer given the GPU's own selection (and, for the
+    # rescue methods, the GPU's rescue tokens: fp32 near-ties may pick another)
+    choice = None
+    if method in attention.RESCUE_METHODS:
+        choice = to_np(kernels.rescue_choice(qg, up.attention_tiles(kg, vg)[0]))
+    want, _ = ref.attention_from_selection(to_np(q), to_np(k), to_np(v), SCALE, method,
+                                           to_np(sel), choice=choice)
+    assert_output_close(to_np(out), want, what=f"{method} d256 (GPU lists)", rel=2.0 ** -7)
     if method not in attention.RESCUE_METHODS:
         assert_output_close(to_np(out), expected["output"], what=f"{method} d256", rel=2.0 ** -7)
 
 
-@pytest.mark.parametrize("length", (385, 2200))
-def test_rescue_choice_d256_vs_oracle(gpu, length):
-    """The rescue token (argmax over a block's positions of the tile's mean query .
-    k, first position on ties) at d = 256: the float64 argmax, except fp32 near-ties
-    (then the GPU's token scores within 1e-5 of the maximum)."""
-    q, k, v = _inputs(length, seed=61)
+@pytest.mark.parametrize("selector", ("mean_balanced", "cgf_mean", "dispersion_mean"))
+@pytest.mark.parametrize("length", (1089, 4500))   # 4500: two 32-block chunks per tile
+def test_selector_scores_d256_vs_oracle(gpu, selector, length):
+    """kernels.py:49-126 at d = 256 (two 128-dim halves per chunk) on unit-scale
+    inputs, as check_math runs its selector check, within its 2e-5 tolerance of
+    the oracle; rows sum to 1 over j < t."""
+    q, k, v, _ = synthetic.make_inputs(length, seed=29, q_heads=Q_HEADS, kv_heads=KV_HEADS,
+                                       head_dim=DIM)
     qg, kg, vg = q.cuda(), k.cuda(), v.cuda()
-    got = to_np(kernels.rescue_choice(qg, up.attention_tiles(kg, vg)[0]))
-    want = ref.rescue_choice(to_np(q), to_np(k))
-    blocks = ref.num_blocks(length)
-    causal = np.arange(blocks)[None, :, None, None] < np.arange(blocks)[None, None, :, None]
-    causal = np.broadcast_to(causal.transpose(0, 2, 1, 3), got.shape)
-    assert (got[~causal] == 0).all()
-    diff = np.argwhere((got != want) & causal)
-    qbar = ref.tile_mean_query(to_np(q)).astype(np.float64)
-    kk = to_np(k).astype(np.float64)
-    group = Q_HEADS // KV_HEADS
-    for b, t, j, h in diff:
-        scores = kk[b, j * 128:(j + 1) * 128, h // group] @ qbar[b, t, h]
-        assert scores.max() - scores[got[b, t, j, h]] <= 1e-5 * (abs(scores.max()) + 1), (t, j, h)
-    assert len(diff) <= max(2, causal.sum() // 1000)
-
-
-@pytest.mark.parametrize("remainder", (False, True))
-def test_rescue_tail_d256_vs_oracle(gpu, remainder):
-    length = 1089
-    q, k, v = _inputs(length, seed=67)
-    qg, kg, vg = q.cuda(), k.cuda(), v.cuda()
-    sel = _sparse_mask(length, seed=11)
-    out, lse = kernels.rescue_tail(qg, kg, vg, torch.from_numpy(sel).cuda(), SCALE,
-                                   remainder=remainder)
-    choice = to_np(kernels.rescue_choice(qg, up.attention_tiles(kg, vg)[0]))
-    e_out, e_lse = ref.rescue_tail(to_np(q), to_np(k), to_np(v), sel, SCALE, remainder=remainder,
-                                   choice=choice)
-    # token values are O(1): bf16 probabilities leave ~2^-8 |v|
-    np.testing.assert_allclose(to_np(out), e_out, atol=1e-2, rtol=2e-2)
-    finite = np.isfinite(e_lse)
-    assert finite.any() and not finite.all()
-    np.testing.assert_array_equal(np.isfinite(to_np(lse)), finite)
-    np.testing.assert_allclose(to_np(lse)[finite], e_lse[finite], atol=2e-3, rtol=1e-3)
+    desc = kernels.block_descriptors(kg, vg)
+    got = to_np(kernels.selector_scores(qg, desc, SCALE, selector))
+    e_desc = ref.block_descriptors(to_np(k), to_np(v))
+    want = ref.selector_scores(to_np(q), e_desc, SCALE, selector)
+    np.testing.assert_allclose(got, want, atol=2e-5, rtol=2e-5)
+    if selector != "dispersion_mean":
+        rows = got[0, 1:].sum(axis=1)
+        np.testing.assert_allclose(rows, 1.0, atol=1e-5)
 
 
 def _sparse_mask(length, seed):

@@ -47,11 +47,12 @@ def test_c_abi_argument_validation_without_gpu():
     assert lib.spx_block_mean_k(odd, s4, 1, 256, 4, 128, 128, fake, None) == _lib.SPX_EINVAL
     assert lib.spx_selector_scores(fake, s4, fake, fake, fake, fake, 1, 256, 28, 4, 128, 128, 7,
                                    ctypes.c_float(0.1), fake, fake, s4, None) == _lib.SPX_EINVAL
-    # a null workspace is rejected; workspace bytes = B Hkv ceil(NB / 32) 32 KB
+    # a null workspace is rejected; workspace bytes = B Hkv ceil(NB / 32) (D / 128) 32 KB
     assert lib.spx_selector_scores(fake, s4, fake, fake, fake, fake, 1, 256, 28, 4, 128, 128, 1,
                                    ctypes.c_float(0.1), None, fake, s4, None) == _lib.SPX_EINVAL
     assert lib.spx_selector_workspace_bytes(1, 32640, 4, 128) == 4 * 8 * 32768
     assert lib.spx_selector_workspace_bytes(2, 4097, 4, 128) == 2 * 4 * 2 * 32768
+    assert lib.spx_selector_workspace_bytes(1, 32640, 4, 256) == 2 * 4 * 8 * 32768
     assert lib.spx_selector_workspace_bytes(1, 256, 4, 64) == -1
     # 28 q heads over 3 kv heads is not a GQA grouping
     assert lib.spx_exact_attention(fake, s4, fake, fake, None, None, None, None, 1, 256, 28, 3,

@@ -31,15 +31,18 @@ def _noalloc(q, desc, selector):
     return scores
 
 
+@pytest.mark.parametrize("head_dim", (128, 256))
 @pytest.mark.parametrize("selector", ("mean_balanced", "cgf_mean", "dispersion_mean"))
-def test_noalloc_matches_workspace_entry_point(gpu, selector):
+def test_noalloc_matches_workspace_entry_point(gpu, selector, head_dim):
+    heads = {"q_heads": 28, "kv_heads": 4} if head_dim == 128 else {"q_heads": 16, "kv_heads": 4}
     for length, seed in ((4500, 3), (1089, 4)):      # the second call is smaller
-        q, k, v, _ = synthetic.make_inputs(length, seed=seed, device="cuda")
+        q, k, v, _ = synthetic.make_inputs(length, seed=seed, head_dim=head_dim, device="cuda",
+                                           **heads)
         desc = kernels.block_descriptors(k, v)
         want = kernels.selector_scores(q, desc, SCALE, selector)
         got = _noalloc(q, desc, selector)
         torch.cuda.synchronize()
-        assert torch.equal(got, want), f"{selector} S={length}"
+        assert torch.equal(got, want), f"{selector} S={length} D={head_dim}"
 
 
 def test_noalloc_refuses_shapes_beyond_the_array(gpu):
