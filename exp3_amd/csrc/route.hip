@@ -133,23 +133,55 @@ __device__ void select_row(const float* row, int t, const SelectParams& p, const
   if (o.counts && tid == 0) o.counts[o.count_off] = base;
 }
 
-// V1 selection (upstream :357-407 with min_budget = 0) of one score row in LDS, by
-// one wave: the same rule as select_row, compacted 64 key blocks per ballot.
-__device__ void select_v1_row_wave(const float* row, int t, const SelectParams& p,
-                                   const SelectOut& o) {
+// Reductions over a wave with DPP row operations (quad permutes, half-row and row
+// mirrors, row broadcasts 15 and 31) instead of LDS-routed lane shuffles; the
+// result is read from lane 63 and is wave-uniform. Lanes a DPP step cannot source
+// take `identity`.
+template <class Op>
+__device__ __forceinline__ float wave_reduce_dpp(float v, float identity, Op op) {
+  const int id = __float_as_int(identity);
+#define SPX_DPP_STEP(ctrl, rows) \
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(v), ctrl, rows, 0xf, false)))
+  SPX_DPP_STEP(0xB1, 0xf);   // quad_perm [1, 0, 3, 2]
+  SPX_DPP_STEP(0x4E, 0xf);   // quad_perm [2, 3, 0, 1]
+  SPX_DPP_STEP(0x141, 0xf);  // row_half_mirror
+  SPX_DPP_STEP(0x140, 0xf);  // row_mirror: every lane of a 16-lane row holds the row's value
+  SPX_DPP_STEP(0x142, 0xa);  // row_bcast 15 into rows 1 and 3
+  SPX_DPP_STEP(0x143, 0xc);  // row_bcast 31 into rows 2 and 3: lane 63 holds the total
+#undef SPX_DPP_STEP
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  return wave_reduce_dpp(v, -INFINITY, [](float a, float b) { return max_nan(a, b); });
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  return wave_reduce_dpp(v, 0.0f, [](float a, float b) { return a + b; });
+}
+
+// V1 selection (upstream :357-407 with min_budget = 0) of one normalised score row
+// held in registers by one wave (block c * 64 + lane in sv[c]): the same rule as
+// select_row, compacted 64 key blocks per ballot.
+constexpr int kRowChunks = kMaxBlocks / 64;
+__device__ __forceinline__ void select_v1_row_regs(const float (&sv)[kRowChunks], int t,
+                                                   const SelectParams& p, const SelectOut& o) {
   const int lane = threadIdx.x & 63;
   const int kb = p.key_blocks;
+  const int nch = (kb + 63) >> 6;
   float local = -INFINITY;
-  for (int j = lane; j < kb; j += 64) local = max_nan(local, row[j]);
-  const float maximum = wave_max(local);
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c)
+    if (c < nch && c * 64 + lane < kb) local = max_nan(local, sv[c]);
+  const float maximum = wave_max_dpp(local);
   const float threshold = maximum * p.alpha;   // fp32(max * fp32(alpha))
   const bool last_rows = t >= p.query_blocks - p.last;
   int base = 0;
-  for (int j0 = 0; j0 < kb; j0 += 64) {
-    const int j = j0 + lane;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    if (c >= nch) break;
+    const int j = c * 64 + lane;
     bool active = false;
     if (j < kb) {
-      const bool keep = row[j] >= threshold;
+      const bool keep = sv[c] >= threshold;
       const int distance = t - j;
       const bool prot = j < p.sink || (distance >= 0 && distance < p.window) || last_rows;
       active = (keep || prot) && distance >= 0;
@@ -410,22 +442,45 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   // cross-wave reductions; the other waves end here.
   if (wave != 0) return;
 
-  // normalize_scores over j <= t; j > t has M = -inf and contributes 0.
+  // normalize_scores over j <= t (j > t has M = -inf and contributes 0), on the row
+  // held in registers: lane holds blocks c * 64 + lane, loops fully unrolled
+  const int nch = (a.blocks + 63) >> 6;
+  float sv[kRowChunks];
   float local = -INFINITY;
-  for (int jj = lane; jj <= t; jj += 64) local = fmaxf(local, blk_max[jj]);
-  const float gmax = wave_max(local);
-  float wsum = 0.0f;
-  for (int jj = lane; jj <= t; jj += 64) {
-    const float m = blk_max[jj];
-    const float w = (m != -INFINITY) ? blk_mass[jj] * exp2_fast(m - gmax) : 0.0f;
-    blk_mass[jj] = w;
-    wsum += w;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    sv[c] = -INFINITY;   // the block's M, then its weight, then its score
+    if (c < nch) {
+      const int jj = c * 64 + lane;
+      if (jj <= t) {
+        sv[c] = blk_max[jj];
+        local = fmaxf(local, sv[c]);
+      }
+    }
   }
-  const float total = wave_sum(wsum) + 1e-9f;
-  for (int jj = lane; jj < a.blocks; jj += 64) {
-    const float s = jj <= t ? blk_mass[jj] / total : 0.0f;
-    blk_mass[jj] = s;
-    if (a.score) a.score[b * a.ss_b + t * a.ss_t + jj * a.ss_j + h * a.ss_h] = s;
+  const float gmax = wave_max_dpp(local);
+  float wsum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    if (c < nch) {
+      const int jj = c * 64 + lane;
+      float w = 0.0f;
+      if (jj <= t) {
+        w = (sv[c] != -INFINITY) ? blk_mass[jj] * exp2_fast(sv[c] - gmax) : 0.0f;
+        wsum += w;
+      }
+      sv[c] = w;
+    }
+  }
+  const float total = wave_sum_dpp(wsum) + 1e-9f;
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    if (c < nch) {
+      const int jj = c * 64 + lane;
+      const float sc = jj <= t ? sv[c] / total : 0.0f;
+      sv[c] = sc;
+      if (a.score && jj < a.blocks) a.score[b * a.ss_b + t * a.ss_t + jj * a.ss_j + h * a.ss_h] = sc;
+    }
   }
   if (a.indices) {
     SelectOut o;
@@ -435,7 +490,7 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
     o.heads = a.q_heads;
     o.row_base = (((int64_t)b * a.blocks + t) * a.blocks) * a.q_heads + h;
     o.count_off = ((int64_t)b * a.blocks + t) * a.q_heads + h;
-    select_v1_row_wave(blk_mass, t, a.sel, o);
+    select_v1_row_regs(sv, t, a.sel, o);
   }
 }
 
