@@ -171,13 +171,6 @@ __device__ __forceinline__ int operand_base(int row) {
   return row * kBlock + (cx << 4) + (hb << 3);
 }
 
-// Keep `x` opaque inside a loop so derived addresses are recomputed per use
-// instead of being hoisted (and held) as a table of loop invariants.
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
 // Compiler fence: nothing is scheduled across it. Keeps operand reads issued a
 // step ahead of the MFMAs that consume them.
 __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
@@ -517,13 +510,6 @@ __device__ __forceinline__ void write_tail_entry(uint16_t* kb, uint16_t* vb, int
     const int d = c * 8 + x;
     vb[swz(d, slot >> 3) + (slot & 7)] = to_bf16_bits(mv[x]);
   }
-}
-
-__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
-  const f32x4 a0 = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 a1 = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) { x[e] = a0[e]; x[4 + e] = a1[e]; }
 }
 
 // Block-mean tail tile: entries t0 .. t0 + 63 of `ids` (unselected blocks), key =

@@ -74,13 +74,6 @@ struct Attn256Args {
   int64_t vs_b, vs_s, vs_h;
 };
 
-// Keep `x` opaque inside a loop so values derived from it are recomputed per use
-// instead of being hoisted (and held in registers) as loop invariants.
-__device__ __forceinline__ int opaque256(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
 // Position of 16-byte chunk c (< 32) of K row r in the d = 256 key layout.
 __device__ __forceinline__ int key_chunk_pos(int r, int c) { return (c & 16) | ((c & 15) ^ (r & 15)); }
 
@@ -166,13 +159,6 @@ __device__ __forceinline__ void key_products(const uint16_t* kb, int e0, const b
     for (int i = 0; i < 4; ++i) sc = mfma32(kr[i], qb[g4 * 4 + i], sc);
     __builtin_amdgcn_sched_barrier(0);
   }
-}
-
-__device__ __forceinline__ void load8f(const float* p, float (&x)[8]) {
-  const f32x4 a0 = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 a1 = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) { x[e] = a0[e]; x[4 + e] = a1[e]; }
 }
 
 // Tail sub-block entry i (< 32), 8-dim chunk c (< 32): key hi / lo rows in kh / kl,
@@ -349,7 +335,7 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
       // would push the wave past 256 registers (AGPR spills, one wave per SIMD)
 #pragma unroll 1
       for (int k4 = 0; k4 < (kSub * (kD2 / 8)) / kA2Threads; ++k4) {
-        const int e = opaque256(tid) + k4 * kA2Threads;
+        const int e = opaque(tid) + k4 * kA2Threads;
         const int i = e >> 5, c = e & 31;
         const int blk = t0 + i / epb, kind = i % epb;
         const int j = blk < ntail ? (int)tlist[blk] : -1;
@@ -358,8 +344,8 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
         if (j >= 0) {
           const int64_t off = (((int64_t)b * a.blocks + j) * a.kv_heads + g) * kD2 + c * 8;
           if (a.tail_kind == 0) {
-            load8f(a.mean_k + off, mk);
-            load8f(a.mean_v + off, mv);
+            load8(a.mean_k + off, mk);
+            load8(a.mean_v + off, mv);
             bi = logf((float)a.bcounts[j]) * kLog2e;
           } else {
             // history blocks j < t are full, so the token is inside the sequence
@@ -382,8 +368,8 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
               bi = 0.0f;
             } else {
               float mean_k[8], mean_v[8];
-              load8f(a.mean_k + off, mean_k);
-              load8f(a.mean_v + off, mean_v);
+              load8(a.mean_k + off, mean_k);
+              load8(a.mean_v + off, mean_v);
 #pragma unroll
               for (int x = 0; x < 8; ++x) {
                 mk[x] = (mean_k[x] * (float)kBlock - kval[x]) / (float)(kBlock - 1);
@@ -397,7 +383,7 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
         if (c == 0) tail_bias[i] = bi;
       }
       block_sync();
-      const int lane_t = opaque256(lane);
+      const int lane_t = opaque(lane);
       const int col_t = lane_t & 31;
       const int e0_t = (((col_t >> 1) & 7) << 4) + (((lane_t >> 5) ^ (col_t & 1)) << 3);
       f32x16 sc = {};

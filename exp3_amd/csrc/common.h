@@ -75,6 +75,21 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) {
 
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32); }
 
+// Keep `x` opaque inside a loop so values derived from it are recomputed per use
+// instead of being hoisted (and held in registers) as loop invariants.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Eight consecutive fp32 values (16-byte aligned) as two 16-byte loads.
+__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+  const f32x4 a0 = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 a1 = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { x[e] = a0[e]; x[4 + e] = a1[e]; }
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o >= 1; o >>= 1) v = max_nan(v, __shfl_xor(v, o));
   return v;

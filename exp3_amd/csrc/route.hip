@@ -177,20 +177,21 @@ __device__ __forceinline__ void select_v1_row_regs(const float (&sv)[kRowChunks]
   int base = 0;
 #pragma unroll
   for (int c = 0; c < kRowChunks; ++c) {
-    if (c >= nch) break;
-    const int j = c * 64 + lane;
-    bool active = false;
-    if (j < kb) {
-      const bool keep = sv[c] >= threshold;
-      const int distance = t - j;
-      const bool prot = j < p.sink || (distance >= 0 && distance < p.window) || last_rows;
-      active = (keep || prot) && distance >= 0;
-      if (o.mask) o.mask[o.row_base + (int64_t)j * o.heads] = active ? 1 : 0;
+    if (c < nch) {   // wave-uniform
+      const int j = c * 64 + lane;
+      bool active = false;
+      if (j < kb) {
+        const bool keep = sv[c] >= threshold;
+        const int distance = t - j;
+        const bool prot = j < p.sink || (distance >= 0 && distance < p.window) || last_rows;
+        active = (keep || prot) && distance >= 0;
+        if (o.mask) o.mask[o.row_base + (int64_t)j * o.heads] = active ? 1 : 0;
+      }
+      const uint64_t ballot = __ballot(active);
+      const int before = __popcll(ballot & ((1ull << lane) - 1ull));
+      if (active && o.indices) o.indices[o.row_base + (int64_t)(base + before) * o.heads] = j;
+      base += __popcll(ballot);
     }
-    const uint64_t ballot = __ballot(active);
-    const int before = __popcll(ballot & ((1ull << lane) - 1ull));
-    if (active && o.indices) o.indices[o.row_base + (int64_t)(base + before) * o.heads] = j;
-    base += __popcll(ballot);
   }
   if (o.indices) {
     for (int pos = base + lane; pos < kb; pos += 64)
