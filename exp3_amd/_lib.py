@@ -18,7 +18,7 @@ SPX_OK = 0
 SPX_EINVAL = -1
 SPX_EUNSUPPORTED = -2
 SPX_ELAUNCH = -3
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 SELECTOR_IDS = {"mean_balanced": 0, "cgf_mean": 1, "dispersion_mean": 2}
 
@@ -44,9 +44,9 @@ _PROTOTYPES = {
     "spx_selector_scores_noalloc": [_P, _S, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _P,
                                     _S, _P],
     "spx_exact_attention": [_P, _S, _P, _P, _P, _S, _P, _S, _I, _I, _I, _I, _I, _I, _F, _P,
-                            _S, _P, _S, _P],
+                            _S, _P, _S, _P, _P],
     "spx_sparse_attention_mean": [_P, _S, _P, _P, _P, _S, _P, _S, _P, _P, _P, _I, _I, _I, _I,
-                                  _I, _I, _F, _P, _S, _P, _S, _P],
+                                  _I, _I, _F, _P, _S, _P, _S, _P, _P],
     "spx_mean_tail": [_P, _S, _P, _S, _P, _S, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _S, _P,
                       _S, _P],
     "spx_merge_exact_mean": [_P, _S, _P, _S, _P, _S, _P, _S, _I, _I, _I, _I, _P, _S, _P, _S, _P],
@@ -56,7 +56,7 @@ _PROTOTYPES = {
     "spx_rescue_tail": [_P, _S, _P, _P, _P, _S, _P, _S, _P, _P, _S, _P, _P, _I, _I, _I, _I, _I,
                         _I, _I, _F, _P, _S, _P, _S, _P],
     "spx_sparse_attention_rescue": [_P, _S, _P, _P, _P, _S, _P, _S, _P, _P, _S, _P, _P, _I, _I,
-                                    _I, _I, _I, _I, _I, _F, _P, _S, _P, _S, _P],
+                                    _I, _I, _I, _I, _I, _F, _P, _S, _P, _S, _P, _P],
 }
 
 # helpers with other return types

@@ -168,11 +168,12 @@ def exact_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         _flash_forward.best_config = _ATTENTION_CONFIGS[head_dim]
     output = torch.empty(batch, sequence, q_heads, head_dim, dtype=q.dtype, device=device)
     lse = torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
+    queue = torch.zeros(1, dtype=torch.int32, device=device)   # dynamic-tail counter
     _lib.call("spx_exact_attention", _lib.ptr(q), _lib.strides(q), _lib.ptr(key_tiles),
               _lib.ptr(value_tiles), _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
               _lib.strides(counts), batch, sequence, q_heads, k.shape[2], head_dim, block_size,
               float(scale), _lib.ptr(output), _lib.strides(output), _lib.ptr(lse),
-              _lib.strides(lse), _lib.stream(device))
+              _lib.strides(lse), _lib.ptr(queue), _lib.stream(device))
     return output, lse
 
 

@@ -38,7 +38,7 @@ extern "C" {
 #define SPX_EUNSUPPORTED (-2) /* valid in the reference, not built here       */
 #define SPX_ELAUNCH (-3)      /* HIP launch / runtime failure                 */
 
-#define SPX_ABI_VERSION 6
+#define SPX_ABI_VERSION 7
 
 /* Selector ids for spx_selector_scores (kernels.py:62). */
 #define SPX_SELECTOR_MEAN_BALANCED 0
@@ -181,6 +181,13 @@ int spx_selector_scores_noalloc(const void* q, const int64_t* q_strides, const f
  * (dense causal attention). out: bf16 [B, S, Hq, D] (strided); lse: natural-log LSE
  * fp32 [B, S, Hq] (strided, may be NULL). List ids outside [0, NB) are skipped;
  * only the block equal to the query tile is masked (key > query). head_dim 128 or 256.
+ * work_queue (optional, here and in the two fused variants below): a 4-byte aligned
+ * device int32 holding 0 when the launch starts; the launch then takes its lightest
+ * third of tile pairs from it in heaviest-first order, which evens out the XCDs
+ * (they run at different speeds; the static deal binds work to an XCD). The value
+ * it is left holding is unspecified: zero it before the next use, and use one
+ * counter per launch in flight. NULL (or head_dim 256, or B * Hkv not dividing 8)
+ * keeps the static schedule; the results are identical either way.
  * Replaces upstream/flashprefill_native_forward.py:478-521 (exact_attention) and the
  * Triton kernel _flash_forward (:215-354). */
 int spx_exact_attention(const void* q, const int64_t* q_strides, const void* key_tiles,
@@ -189,7 +196,8 @@ int spx_exact_attention(const void* q, const int64_t* q_strides, const void* key
                         const int32_t* counts, const int64_t* count_strides, int batch,
                         int seq, int q_heads, int kv_heads, int head_dim, int block_size,
                         float scale, void* out, const int64_t* out_strides, float* lse,
-                        const int64_t* lse_strides, void* stream);
+                        const int64_t* lse_strides, int32_t* work_queue,
+                        void* stream);
 
 /* Exact attention with the block-mean correction fused in: each row additionally
  * attends to the fp32 mean K / mean V (logit + ln n_j) of every full-history block
@@ -207,7 +215,8 @@ int spx_sparse_attention_mean(const void* q, const int64_t* q_strides, const voi
                               const int32_t* block_counts, int batch, int seq, int q_heads,
                               int kv_heads, int head_dim, int block_size, float scale,
                               void* out, const int64_t* out_strides, float* lse,
-                              const int64_t* lse_strides, void* stream);
+                              const int64_t* lse_strides, int32_t* work_queue,
+                              void* stream);
 
 /* Mean path alone: fp32 output and LSE of each row against the mean K / V of the
  * unselected full-history blocks of its tile (selection given as index lists,
@@ -279,7 +288,8 @@ int spx_sparse_attention_rescue(const void* q, const int64_t* q_strides, const v
                                 int batch, int seq, int q_heads, int kv_heads, int head_dim,
                                 int block_size, float scale, void* out,
                                 const int64_t* out_strides, float* lse,
-                                const int64_t* lse_strides, void* stream);
+                                const int64_t* lse_strides, int32_t* work_queue,
+                                void* stream);
 
 /* ----------------------------------------------------------- accounting */
 

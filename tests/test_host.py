@@ -56,7 +56,7 @@ def test_c_abi_argument_validation_without_gpu():
     assert lib.spx_selector_workspace_bytes(1, 256, 4, 64) == -1
     # 28 q heads over 3 kv heads is not a GQA grouping
     assert lib.spx_exact_attention(fake, s4, fake, fake, None, None, None, None, 1, 256, 28, 3,
-                                   128, 128, ctypes.c_float(0.1), fake, s4, None, None,
+                                   128, 128, ctypes.c_float(0.1), fake, s4, None, None, None,
                                    None) == _lib.SPX_EINVAL
     # 131073 tokens exceed the 1024-block limit of the routing kernels
     assert lib.spx_v1_scores(fake, s4, fake, s4, 1, 131073, 28, 4, 128, 128, ctypes.c_float(0.1),
