@@ -1036,7 +1036,7 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
   if (lse) SPX_REQUIRE(lse_strides != nullptr, SPX_EINVAL, "lse strides missing");
   if (head_dim == 256) {
     const Attn256Options opt{req.exact, req.tail, req.out_f32, req.tail_kind, mean_k, mean_v,
-                             block_counts, req.choice, req.v, req.v_strides};
+                             block_counts, req.choice, req.v, req.v_strides, req.work_queue};
     return launch_attention_256(opt, q, q_strides, key_tiles, value_tiles, indices, index_strides,
                                 counts, count_strides, batch, seq, q_heads, kv_heads, scale, out,
                                 out_strides, lse, lse_strides, stream);

@@ -72,6 +72,10 @@ struct Attn256Args {
   const uint8_t* choice;
   const uint16_t* v;
   int64_t vs_b, vs_s, vs_h;
+  // dynamic tail: tile ranks >= static_ranks are taken from a zeroed counter
+  int* queue;          // null: every workgroup on the static grid
+  int static_ranks;
+  int dyn_items;
 };
 
 // Position of 16-byte chunk c (< 32) of K row r in the d = 256 key layout.
@@ -211,8 +215,20 @@ __device__ __forceinline__ void dma_16k(const uint16_t* src, uint16_t* lds, int 
 template <bool EXACT, bool TAIL, bool OUT_F32>
 __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
   const int per_tile = a.batch * a.q_heads;
-  const int t = a.blocks - 1 - (int)(blockIdx.x / per_tile);  // heaviest tiles first
-  const int bh = blockIdx.x % per_tile;
+  int rank = (int)(blockIdx.x / per_tile), bh = (int)(blockIdx.x % per_tile);
+  if (a.queue && rank >= a.static_ranks) {
+    // dynamic tail: XCDs run at different speeds and workgroup i is bound to XCD
+    // i % 8, so the light tiles go to whichever workgroups run first (surplus ones
+    // find the counter past the end and exit)
+    __shared__ int dyn_k;
+    if (threadIdx.x == 0) dyn_k = atomicAdd(a.queue, 1);
+    block_sync();
+    const int kd = dyn_k;
+    if (kd >= a.dyn_items) return;
+    rank = a.static_ranks + kd / per_tile;
+    bh = kd % per_tile;
+  }
+  const int t = a.blocks - 1 - rank;  // heaviest tiles first
   const int b = bh / a.q_heads, h = bh % a.q_heads;
   const int g = h / (a.q_heads / a.kv_heads);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -468,7 +484,15 @@ int launch_attention_256(const Attn256Options& opt, const void* q, const int64_t
       a.vs_b = opt.v_strides[0]; a.vs_s = opt.v_strides[1]; a.vs_h = opt.v_strides[2];
     }
   }
-  const unsigned grid = (unsigned)(blocks * batch * q_heads);
+  unsigned grid = (unsigned)(blocks * batch * q_heads);
+  if (opt.work_queue) {
+    SPX_REQUIRE((reinterpret_cast<uintptr_t>(opt.work_queue) & 3) == 0, SPX_EINVAL,
+                "work_queue must be 4-byte aligned");
+    a.queue = opt.work_queue;
+    a.static_ranks = blocks * 2 / 3;
+    a.dyn_items = (blocks - a.static_ranks) * batch * q_heads;
+    grid = (unsigned)(a.static_ranks * batch * q_heads) + (unsigned)((a.dyn_items * 5 + 3) / 4);
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (opt.exact && !opt.tail) attn256_kernel<true, false, false><<<grid, kA2Threads, 0, st>>>(a);
   else if (opt.exact) attn256_kernel<true, true, false><<<grid, kA2Threads, 0, st>>>(a);

@@ -144,6 +144,7 @@ struct Attn256Options {
   const uint8_t* choice;       // [B, NB, NB, Hq] rescue token per (tile, block, head)
   const void* v;               // V rows of the rescue tokens, strided [B, S, Hkv, 256]
   const int64_t* v_strides;
+  int32_t* work_queue;         // optional zeroed counter: the last third of the tiles dealt dynamically
 };
 // Attention at head_dim 256 (attn256.hip); arguments as spx_exact_attention and the
 // tail entry points, already validated by the caller.
