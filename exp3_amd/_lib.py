@@ -18,7 +18,9 @@ SPX_OK = 0
 SPX_EINVAL = -1
 SPX_EUNSUPPORTED = -2
 SPX_ELAUNCH = -3
-ABI_VERSION = 7
+ABI_VERSION = 8
+# int32 counters behind the attention entry points' work_queue (SPX_WORK_QUEUE_INTS)
+WORK_QUEUE_INTS = 16
 
 SELECTOR_IDS = {"mean_balanced": 0, "cgf_mean": 1, "dispersion_mean": 2}
 

@@ -218,8 +218,8 @@ class AttentionBackend:
         common_head = (_lib.ptr(q), _lib.strides(q), _lib.ptr(tiles[0]), _lib.ptr(tiles[1]),
                        _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
                        _lib.strides(counts))
-        # zeroed counter for the kernel's dynamic tail (XCD load balance)
-        queue = torch.zeros(1, dtype=torch.int32, device=device)
+        # zeroed counters of the kernel's persistent grid (work items taken in turn)
+        queue = torch.zeros(_lib.WORK_QUEUE_INTS, dtype=torch.int32, device=device)
         common_tail = (batch, sequence, q_heads, k.shape[2], head_dim, self.block_size,
                        float(scale), _lib.ptr(output), _lib.strides(output), _lib.ptr(lse),
                        _lib.strides(lse), _lib.ptr(queue), _lib.stream(device))

@@ -37,7 +37,9 @@
 //     i % 8; a (batch, kv group) stream is served by a fixed set of XCDs, so the q
 //     heads sharing a KV block read it from the same L2s, and with 8 / (B * Hkv)
 //     XCDs per stream the heads of each tile pair are dealt over that set in turn,
-//     which keeps the XCDs' shares of the work equal.
+//     which keeps the XCDs' shares of the work equal. Given a work queue, the grid
+//     is persistent: one workgroup per CU takes its XCD's items in that order from
+//     a counter, then the light last third of the tile pairs from a shared one.
 #include <type_traits>
 
 #include "common.h"
@@ -79,12 +81,13 @@ struct AttnArgs {
   int batch, seq, q_heads, kv_heads, blocks, group, num_pairs;
   int xcds_per_stream;   // XCDs sharing one (batch, kv group) stream; 1: pair p on XCD p % 8
   float scale_log2;
-  // dynamic tail (xcds_per_stream > 1 and a caller queue): the light tile pairs are
-  // taken from a queue in heaviest-first order by whichever workgroups run first
-  int* queue;        // zeroed int32 (null: every workgroup on the static mapping)
-  int static_local;  // workgroups per XCD on the static mapping
-  int dyn_tp0;       // first tile pair of the dynamic tail
-  int dyn_items;     // its (tile pair, q head) items
+  // Persistent grid (a caller queue): one workgroup per CU takes items until none
+  // are left. Tile pairs [0, static_tp) are dealt to XCDs as in the static grid and
+  // taken in order through XCD x's counter queue[1 + x]; the rest (the lightest) go
+  // through queue[0] in heaviest-first order to whichever XCD asks first.
+  int* queue;        // SPX_WORK_QUEUE_INTS zeroed int32 (null: one workgroup per item)
+  int static_tp;     // tile pairs on the per-XCD deal (all of them without a queue)
+  int dyn_items;     // (tile pair, stream, head) items of the shared tail
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) {
@@ -165,13 +168,17 @@ __device__ __forceinline__ void dma_part(const uint16_t* src, uint16_t* lds, int
       : "memory");
 }
 
+// threadIdx.x behind an opaque copy: values derived from it are recomputed for
+// every work item of a persistent workgroup instead of being held across items.
+__device__ __forceinline__ int thread_x() { return opaque((int)threadIdx.x); }
+
 __device__ __forceinline__ void wait_tiles() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // LDS element offset of this lane's MFMA operand row (row & 15 == col & 15 for
 // every operand row it reads) with 16-byte chunk 2 x + half, for x = 0: the chunk
 // for any other x is base ^ (x << 4) (XOR swizzle c ^ (row & 15), c = 2 x + half).
 __device__ __forceinline__ int operand_base(int row) {
-  const int lane = threadIdx.x & 63;
+  const int lane = thread_x() & 63;
   const int col = lane & 31, half = lane >> 5;
   const int cx = (col >> 1) & 7, hb = half ^ (col & 1);
   return row * kBlock + (cx << 4) + (hb << 3);
@@ -188,7 +195,7 @@ template <int NMB, bool HILO>
 __device__ __forceinline__ void scores(const uint16_t* kb, const WaveState& ws, int row0,
                                        f32x16 (&s)[4]) {
   constexpr int P = NMB * (HILO ? 2 : 1);
-  const int col = threadIdx.x & 31;
+  const int col = thread_x() & 31;
   const int e0 = opaque(operand_base(row0 + col));
   auto row_off = [](int part) {
     return HILO ? ((part & 1) ? kTailTile * kBlock : 0) + (part >> 1) * 32 * kBlock
@@ -222,7 +229,7 @@ __device__ __forceinline__ void scores(const uint16_t* kb, const WaveState& ws, 
 template <int NMB, bool DIAG, bool BIAS>
 __device__ __forceinline__ void softmax(f32x16 (&s)[4], WaveState& ws, float scale, int q_pos,
                                         const float* bias, int bias_row0, bf16x8 (&pb)[8]) {
-  const int lane = threadIdx.x & 63;
+  const int lane = thread_x() & 63;
   float mx = -INFINITY;
 #pragma unroll
   for (int mb = 0; mb < NMB; ++mb) {
@@ -272,7 +279,7 @@ __device__ __forceinline__ void softmax(f32x16 (&s)[4], WaveState& ws, float sca
 template <int NKC>
 __device__ __forceinline__ void accumulate_pv(const uint16_t* vb, WaveState& ws,
                                               const bf16x8 (&pb)[8]) {
-  const int col = threadIdx.x & 31;
+  const int col = thread_x() & 31;
   const int e0 = opaque(operand_base(col));
   bf16x8 ring[2][4];
 #pragma unroll
@@ -339,7 +346,7 @@ __device__ __forceinline__ bf16x8 lds_at(uint32_t byte_address) {
 
 __device__ __forceinline__ OperandTables operand_tables(const uint16_t* k0, const uint16_t* v0) {
   OperandTables t;
-  const int e0 = operand_base(threadIdx.x & 31);
+  const int e0 = operand_base(thread_x() & 31);
   const uint32_t kb = lds_address(k0), vb = lds_address(v0);
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
@@ -593,18 +600,13 @@ __device__ __forceinline__ void stage_rescue(const AttnArgs& a, const int16_t* i
   }
 }
 
-template <bool EXACT, bool TAIL, bool OUT_F32>
-__global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
-  // ---- work item: query tiles (t, t - 1) of one q head. Tile pairs heaviest first;
-  // workgroup i runs on XCD i % 8, and each XCD serves one (batch, kv group) stream
-  // (or a few when there are more than 8), so the q heads sharing a KV block read
-  // it from one L2.
-  const int p = blockIdx.x;
-  const int xcd = p & 7;
-  const int local = p >> 3;
+// Item decode, static deal: XCD x's local item l. Every XCD serves one (batch, kv
+// group) stream (or a few when there are more than 8), so the q heads sharing a KV
+// block read it from one L2; tile pairs heaviest first.
+__device__ __forceinline__ void static_item(const AttnArgs& a, int xcd, int local, int& pair,
+                                            int& hg) {
   const int bg = a.batch * a.kv_heads;
-  int pair, hg;
-  if (a.xcds_per_stream > 1 && (a.queue == nullptr || local < a.static_local)) {
+  if (a.xcds_per_stream > 1) {
     // (batch, kv group) stream s runs on the xcds_per_stream XCDs x = s (mod bg); its
     // items k = tp * group + hg (heaviest first) are dealt over them in turn, so the
     // heads of a tile pair alternate between those XCDs and every XCD's share of
@@ -615,28 +617,79 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
     const int tpk = k / a.group;
     hg = k - tpk * a.group;
     pair = tpk * bg + s;
-  } else if (a.xcds_per_stream > 1) {
-    // Dynamic tail. XCDs run at different speeds (one launch measured a 6 % spread
-    // in their summed workgroup times), and workgroup i is bound to XCD i % 8, so a
-    // static deal leaves the fast XCDs idle at the end. Every XCD gets more tail
-    // workgroups than its even share; each takes the next item, (tile pair, stream,
-    // head) heaviest first, and those that find the queue empty end at once.
-    __shared__ int dyn_k;
-    if (threadIdx.x == 0) dyn_k = atomicAdd(a.queue, 1);
-    block_sync();
-    const int kd = dyn_k;
-    if (kd >= a.dyn_items) return;
-    const int per_tp = bg * a.group;
-    const int tpk = a.dyn_tp0 + kd / per_tp;
-    const int rem = kd - (tpk - a.dyn_tp0) * per_tp;
-    hg = rem % a.group;
-    pair = tpk * bg + rem / a.group;
   } else {
     const int pair_local = local / a.group;
     hg = local - pair_local * a.group;
     pair = pair_local * 8 + xcd;
   }
+}
+
+// Item decode, shared tail: item kd of tile pairs static_tp.., (tile pair, stream,
+// head) heaviest first.
+__device__ __forceinline__ void tail_item(const AttnArgs& a, int kd, int& pair, int& hg) {
+  const int bg = a.batch * a.kv_heads;
+  const int per_tp = bg * a.group;
+  const int tpk = a.static_tp + kd / per_tp;
+  const int rem = kd - (tpk - a.static_tp) * per_tp;
+  hg = rem % a.group;
+  pair = tpk * bg + rem / a.group;
+}
+
+template <bool EXACT, bool TAIL, bool OUT_F32>
+__device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg);
+
+// Workgroup i runs on XCD i % 8. Without a queue every workgroup runs the one item
+// the static deal gives it. With one, the grid is persistent: launching a workgroup
+// costs a few microseconds, and each XCD starts its workgroups in blockIdx order, a
+// batch of four at a time (one per shader engine), so with short items CUs idled
+// 11 us on average between workgroups (sparse layers). XCDs also run at different
+// speeds (one launch measured a 6 % spread in their summed workgroup times); the
+// shared tail lets the fast ones take more of the light items.
+template <bool EXACT, bool TAIL, bool OUT_F32>
+__global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs args) {
+  const int xcd = blockIdx.x & 7;
+  __shared__ int next_item;
+  for (int round = 0;; ++round) {
+    // The arguments are read afresh for every item through an opaque pointer, so
+    // nothing derived from them is held in registers across items.
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __attribute__((address_space(4))) AttnArgs* ap =
+        (const __attribute__((address_space(4))) AttnArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    const AttnArgs a = *ap;
+#else
+    const AttnArgs a = args;
+#endif
+    int pair, hg;
+    if (a.queue == nullptr) {
+      if (round > 0) break;
+      static_item(a, xcd, blockIdx.x >> 3, pair, hg);
+    } else {
+      const int bg = a.batch * a.kv_heads;
+      const int n_static = a.xcds_per_stream > 1
+          ? a.static_tp * a.group / a.xcds_per_stream
+          : max(0, (a.static_tp * bg - xcd + 7) / 8) * a.group;
+      if (threadIdx.x == 0) {
+        int k = atomicAdd(a.queue + 1 + xcd, 1);
+        if (k >= n_static) k = n_static + atomicAdd(a.queue, 1);
+        next_item = k;
+      }
+      block_sync();
+      const int k = next_item;
+      block_sync();  // read by every wave before thread 0 takes the next one
+      if (k < n_static) static_item(a, xcd, k, pair, hg);
+      else if (k - n_static < a.dyn_items) tail_item(a, k - n_static, pair, hg);
+      else break;
+    }
+    attn_item<EXACT, TAIL, OUT_F32>(a, pair, hg);
+  }
+}
+
+// ---- work item: query tiles (t, t - 1) of one q head
+template <bool EXACT, bool TAIL, bool OUT_F32>
+__device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
   if (pair >= a.num_pairs) return;
+  const int bg = a.batch * a.kv_heads;
   const int tp = pair / bg;                          // tile pair: tiles NB-1-2tp, NB-2-2tp
   const int b = (pair % bg) / a.kv_heads;
   const int g = (pair % bg) % a.kv_heads;
@@ -653,7 +706,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
   __shared__ float tail_bias[2][kTailTile];
   __shared__ int wave_counts[kAttnThreads / 64];
 
-  const int tid = threadIdx.x;
+  const int tid = thread_x();
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int item = w >> 2;                           // 0: tile t, 1: tile t - 1
@@ -865,12 +918,13 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
       }
     }
   }
-
-  // ---- epilogue
+  // ---- epilogue (lane values re-derived: nothing is kept across the block loops)
   const float l = ws.l + xor32(ws.l);
   const bool any = l > 0.0f;
   const float inv = any ? 1.0f / l : 0.0f;
-  const int64_t qrow = (int64_t)t * kBlock + q_pos;
+  const int tx = thread_x();
+  const int half_e = (tx >> 5) & 1;
+  const int64_t qrow = (int64_t)t * kBlock + ((tx >> 6) & 3) * 32 + (tx & 31);
   if (live && qrow < a.seq) {
     if (OUT_F32) {
       float* dst = static_cast<float*>(a.out) + b * a.os_b + qrow * a.os_s + h * a.os_h;
@@ -878,7 +932,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
       for (int db = 0; db < 4; ++db) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const int d0 = db * 32 + 8 * rr + 4 * half;
+          const int d0 = db * 32 + 8 * rr + 4 * half_e;
           *reinterpret_cast<f32x4*>(dst + d0) =
               f32x4{ws.o[db][4 * rr] * inv, ws.o[db][4 * rr + 1] * inv, ws.o[db][4 * rr + 2] * inv,
                     ws.o[db][4 * rr + 3] * inv};
@@ -890,7 +944,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
       for (int db = 0; db < 4; ++db) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const int d0 = db * 32 + 8 * rr + 4 * half;
+          const int d0 = db * 32 + 8 * rr + 4 * half_e;
           u32x2 v2;
           v2[0] = pack_bf16x2(ws.o[db][4 * rr] * inv, ws.o[db][4 * rr + 1] * inv);
           v2[1] = pack_bf16x2(ws.o[db][4 * rr + 2] * inv, ws.o[db][4 * rr + 3] * inv);
@@ -898,7 +952,7 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs a) {
         }
       }
     }
-    if (a.lse && half == 0)
+    if (a.lse && half_e == 0)
       a.lse[b * a.ls_b + qrow * a.ls_s + h * a.ls_h] = any ? ws.m * kLn2 + logf(l) : -INFINITY;
   }
 }
@@ -977,14 +1031,28 @@ struct AttnRequest {
   const uint8_t* choice;     // rescue tokens (tail_kind > 0)
   const void* v;             // V rows of the rescue tokens (tail_kind > 0)
   const int64_t* v_strides;
-  int32_t* work_queue;       // optional zeroed counter for the dynamic tail
+  int32_t* work_queue;       // optional SPX_WORK_QUEUE_INTS zeroed int32: persistent grid
 };
 
-// Dynamic tail: the last third of the tile pairs (the lightest: their lists are the
-// shortest) go through the queue, with 1.25 x an even share of tail workgroups per
-// XCD. Measured on the dense 32640-token layer: 6.81-6.85 -> 6.60-6.64 ms.
+// Persistent grid: the last third of the tile pairs (the lightest: their lists are
+// the shortest) form the shared tail.
 constexpr int kStaticThirds = 2;
-constexpr double kTailOversubscription = 1.25;
+
+// Workgroups per XCD of the persistent grid: one per CU (the kernel's LDS and
+// registers admit one workgroup per CU).
+int persistent_per_xcd() {
+  static int per_device[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
+  if (per_device[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < 8)
+      cus = 256;
+    per_device[dev] = cus / 8;
+  }
+  return per_device[dev];
+}
 
 int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_strides,
                      const void* key_tiles, const void* value_tiles,
@@ -1070,22 +1138,21 @@ int launch_attention(const AttnRequest& req, const void* q, const int64_t* q_str
   a.scale_log2 = (float)((double)scale * 1.4426950408889634);
   const int streams = batch * kv_heads;
   a.xcds_per_stream = (streams <= 8 && 8 % streams == 0) ? 8 / streams : 1;
+  const int np = (blocks + 1) / 2;
   const int per_xcd = a.xcds_per_stream > 1
-      ? ((blocks + 1) / 2 * a.group + a.xcds_per_stream - 1) / a.xcds_per_stream
+      ? (np * a.group + a.xcds_per_stream - 1) / a.xcds_per_stream
       : (a.num_pairs + 7) / 8 * a.group;
+  a.static_tp = np;
   int grid = 8 * per_xcd;
-  if (req.work_queue && a.xcds_per_stream > 1) {
+  if (req.work_queue) {
     SPX_REQUIRE((reinterpret_cast<uintptr_t>(req.work_queue) & 3) == 0, SPX_EINVAL,
                 "work_queue must be 4-byte aligned");
-    const int np = (blocks + 1) / 2;
     int tp0 = np * kStaticThirds / 3;
-    while (tp0 > 0 && (tp0 * a.group) % a.xcds_per_stream) --tp0;
+    while (tp0 > 0 && a.xcds_per_stream > 1 && (tp0 * a.group) % a.xcds_per_stream) --tp0;
     a.queue = req.work_queue;
-    a.static_local = tp0 * a.group / a.xcds_per_stream;
-    a.dyn_tp0 = tp0;
+    a.static_tp = tp0;
     a.dyn_items = (np - tp0) * streams * a.group;
-    const int dyn_per_xcd = (int)((a.dyn_items * kTailOversubscription + 7) / 8);
-    grid = 8 * (a.static_local + dyn_per_xcd);
+    grid = 8 * std::min(persistent_per_xcd(), per_xcd);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (req.exact && !req.tail) attn_kernel<true, false, false><<<grid, kAttnThreads, 0, st>>>(a);

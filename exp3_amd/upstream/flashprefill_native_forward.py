@@ -168,7 +168,7 @@ def exact_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         _flash_forward.best_config = _ATTENTION_CONFIGS[head_dim]
     output = torch.empty(batch, sequence, q_heads, head_dim, dtype=q.dtype, device=device)
     lse = torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
-    queue = torch.zeros(1, dtype=torch.int32, device=device)   # dynamic-tail counter
+    queue = torch.zeros(_lib.WORK_QUEUE_INTS, dtype=torch.int32, device=device)  # work counters
     _lib.call("spx_exact_attention", _lib.ptr(q), _lib.strides(q), _lib.ptr(key_tiles),
               _lib.ptr(value_tiles), _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
               _lib.strides(counts), batch, sequence, q_heads, k.shape[2], head_dim, block_size,

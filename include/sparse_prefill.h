@@ -38,7 +38,10 @@ extern "C" {
 #define SPX_EUNSUPPORTED (-2) /* valid in the reference, not built here       */
 #define SPX_ELAUNCH (-3)      /* HIP launch / runtime failure                 */
 
-#define SPX_ABI_VERSION 7
+#define SPX_ABI_VERSION 8
+
+/* int32 counters a work_queue argument of the attention entry points points to. */
+#define SPX_WORK_QUEUE_INTS 16
 
 /* Selector ids for spx_selector_scores (kernels.py:62). */
 #define SPX_SELECTOR_MEAN_BALANCED 0
@@ -182,12 +185,14 @@ int spx_selector_scores_noalloc(const void* q, const int64_t* q_strides, const f
  * fp32 [B, S, Hq] (strided, may be NULL). List ids outside [0, NB) are skipped;
  * only the block equal to the query tile is masked (key > query). head_dim 128 or 256.
  * work_queue (optional, here and in the two fused variants below): a 4-byte aligned
- * device int32 holding 0 when the launch starts; the launch then takes its lightest
- * third of tile pairs from it in heaviest-first order, which evens out the XCDs
- * (they run at different speeds; the static deal binds work to an XCD). The value
- * it is left holding is unspecified: zero it before the next use, and use one
- * counter per launch in flight. NULL (or head_dim 256, or B * Hkv not dividing 8)
- * keeps the static schedule; the results are identical either way.
+ * device array of SPX_WORK_QUEUE_INTS int32, all 0 when the launch starts. With it
+ * the head_dim 128 kernel runs a persistent grid (one workgroup per CU taking work
+ * items from these counters: no workgroup launch gaps between items, and the fast
+ * XCDs take more of the light last third of the tile pairs); at head_dim 256 the
+ * last third of the tiles is taken from work_queue[0] the same way. The values it
+ * is left holding are unspecified: zero it before the next use, and use one array
+ * per launch in flight. NULL keeps one workgroup per item; the results are
+ * identical either way.
  * Replaces upstream/flashprefill_native_forward.py:478-521 (exact_attention) and the
  * Triton kernel _flash_forward (:215-354). */
 int spx_exact_attention(const void* q, const int64_t* q_strides, const void* key_tiles,

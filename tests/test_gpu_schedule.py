@@ -1,11 +1,13 @@
-"""The attention kernel's dynamic tail (work_queue): the light third of the tile
-pairs taken from a zeroed counter by whichever workgroups run first, to even out
-the XCDs. Results must be bit-identical to the static schedule (the same items,
-each computed by one workgroup with the same arithmetic), every item must be taken
-exactly once (the counter ends at the tail's item count plus the surplus
-workgroups that found it empty), and layouts with (batch x kv heads) not a proper
-divisor of 8 keep the static schedule (d = 128); the d = 256 kernel deals its last
-third of tile ranks the same way."""
+"""The attention kernel's work queue (work_queue): with it the d = 128 kernel runs a
+persistent grid, one workgroup per CU taking (tile pair, head) items in turn: the
+first two thirds of the tile pairs from its own XCD's counter in the static deal's
+order, the light last third from one shared counter. Results must be bit-identical
+to the one-item-per-workgroup grid (the same items, each computed by one workgroup
+with the same arithmetic), and every item must be taken exactly once: each loop
+round of a workgroup draws once from its XCD's counter and, once that share is
+used up, once from the shared counter, so the counters end at the item counts
+plus one failed draw per workgroup. The d = 256 kernel deals its last third of tile
+ranks through the shared counter with 1.25 x as many tail workgroups as items."""
 
 import numpy as np
 import pytest
@@ -53,30 +55,36 @@ def test_dynamic_tail_matches_static_schedule(gpu, layout, entry):
     if entry == "exact" and length == 32640:
         idx = cnt = None     # dense: every causal block
     static = _call(entry, q, k, tiles, idx, cnt, desc, None)
-    queue = torch.zeros(1, dtype=torch.int32, device="cuda")
+    queue = torch.zeros(_lib.WORK_QUEUE_INTS, dtype=torch.int32, device="cuda")
     dynamic = _call(entry, q, k, tiles, idx, cnt, desc, queue)
     torch.cuda.synchronize()
     assert torch.equal(static[0], dynamic[0]) and torch.equal(static[1], dynamic[1])
     assert not torch.isnan(dynamic[0]).any()
     blocks = (length + 127) // 128
     streams = batch * kv_heads
-    taken = int(queue.item())
+    group = q_heads // kv_heads
+    counters = queue.cpu().numpy().astype(np.int64)
     if head_dim == 256:
-        # one workgroup per (tile, head): the last third of the tile ranks dynamic,
-        # 1.25 x as many tail workgroups as items
         items = (blocks - blocks * 2 // 3) * batch * q_heads
-        assert taken == (items * 5 + 3) // 4 >= items
+        assert counters[0] == (items * 5 + 3) // 4 >= items
+        assert not counters[1:].any()
         return
-    per_stream_xcds = 8 // streams if streams <= 8 and 8 % streams == 0 else 1
-    if per_stream_xcds > 1:
-        # kernel constants: the first two thirds of the tile pairs static, 1.25 x an even
-        # share of tail workgroups per XCD
-        np_ = (blocks + 1) // 2
-        tp0 = np_ * 2 // 3
-        while tp0 > 0 and (tp0 * (q_heads // kv_heads)) % per_stream_xcds:
-            tp0 -= 1
-        items = (np_ - tp0) * streams * (q_heads // kv_heads)
-        workgroups = 8 * int((items * 1.25 + 7) // 8)
-        assert taken == workgroups >= items
+    # kernel constants: two thirds of the tile pairs on the per-XCD deal (rounded down
+    # to whole XCD shares), one workgroup per CU, at most one per static item
+    np_ = (blocks + 1) // 2
+    xps = 8 // streams if streams <= 8 and 8 % streams == 0 else 1
+    tp0 = np_ * 2 // 3
+    while tp0 > 0 and xps > 1 and (tp0 * group) % xps:
+        tp0 -= 1
+    per_xcd = (np_ * group + xps - 1) // xps if xps > 1 else (np_ * streams + 7) // 8 * group
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    grid = 8 * min(cus // 8, per_xcd)
+    if xps > 1:
+        static_items = 8 * (tp0 * group // xps)
     else:
-        assert taken == 0          # static schedule: the counter is not touched
+        static_items = sum(max(0, (tp0 * streams - x + 7) // 8) * group for x in range(8))
+    tail_items = (np_ - tp0) * streams * group
+    assert static_items + tail_items == np_ * streams * group
+    assert counters[0] == tail_items + grid
+    assert counters[1:9].sum() == static_items + tail_items + grid
+    assert not counters[9:].any()
