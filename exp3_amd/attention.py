@@ -207,14 +207,17 @@ class AttentionBackend:
     # --------------------------------------------------------- attention
 
     def _attention(self, q, k, tiles, indices, counts, scale, descriptors: BlockDescriptors | None,
-                   rescue=None):
+                   rescue=None, want_lse=True):
         """One attention-kernel launch: exact blocks, plus the block-mean tail
         (``descriptors``) or the rescue tail (``rescue`` = (choice, remainder,
-        descriptors-or-None, v)) in the same online softmax."""
+        descriptors-or-None, v)) in the same online softmax. Returns (output, lse);
+        lse is None when not wanted (the layer discards it, and the kernel then
+        skips its stores)."""
         device = q.device
         batch, sequence, q_heads, head_dim = q.shape
         output = torch.empty(batch, sequence, q_heads, head_dim, dtype=q.dtype, device=device)
-        lse = torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
+        lse = (torch.empty(batch, sequence, q_heads, dtype=torch.float32, device=device)
+               if want_lse else None)
         common_head = (_lib.ptr(q), _lib.strides(q), _lib.ptr(tiles[0]), _lib.ptr(tiles[1]),
                        _lib.ptr(indices), _lib.strides(indices), _lib.ptr(counts),
                        _lib.strides(counts))
@@ -247,7 +250,7 @@ class AttentionBackend:
 
     def _dense_hip(self, q, k, v, scale):
         _, _, tiles = self._pool(k, v, False, False, True)
-        return self._attention(q, k, tiles, None, None, scale, None)
+        return self._attention(q, k, tiles, None, None, scale, None, want_lse=False)
 
     def forward(
         self,
@@ -323,7 +326,8 @@ class AttentionBackend:
                 rescue = (choice, self.method == "fp_v1_rescue_v2", descriptors, v)
             output, _ = self._stage(
                 record, "exact",
-                lambda: self._attention(q, k, tiles, indices, counts, scale, mean_desc, rescue))
+                lambda: self._attention(q, k, tiles, indices, counts, scale, mean_desc, rescue,
+                                        want_lse=False))
             if self.record:
                 q_tile, k_tile = upstream.attention_tile_sizes()
                 score_tile = upstream.score_tile_size() if self.method in V1_ROUTED_METHODS else None

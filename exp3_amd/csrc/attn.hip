@@ -924,9 +924,10 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
   const float inv = any ? 1.0f / l : 0.0f;
   const int tx = thread_x();
   const int half_e = (tx >> 5) & 1;
-  const int64_t qrow = (int64_t)t * kBlock + ((tx >> 6) & 3) * 32 + (tx & 31);
-  if (live && qrow < a.seq) {
-    if (OUT_F32) {
+  const int wq = (tx >> 6) & 3;                       // wave inside its item
+  const int64_t qrow = (int64_t)t * kBlock + wq * 32 + (tx & 31);
+  if (OUT_F32) {
+    if (live && qrow < a.seq) {
       float* dst = static_cast<float*>(a.out) + b * a.os_b + qrow * a.os_s + h * a.os_h;
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
@@ -938,23 +939,40 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
                     ws.o[db][4 * rr + 3] * inv};
         }
       }
-    } else {
-      uint16_t* dst = static_cast<uint16_t*>(a.out) + b * a.os_b + qrow * a.os_s + h * a.os_h;
+    }
+  } else {
+    // Each lane holds 4-dim pieces of its query row, so stored directly every store
+    // instruction would write 16 bytes into each of 32 rows (cache lines). The wave
+    // stages its 32 x 128 bf16 tile in LDS (8 KB per wave in the K buffers, 16-byte
+    // chunk c of row r at c ^ (r & 15)) and stores whole rows: 16 lanes per 256-byte
+    // row, 8 store instructions per wave.
+    block_sync();   // every wave is done with the K / V buffers
+    uint16_t* stage = &kbuf[0][0] + __builtin_amdgcn_readfirstlane(tx >> 6) * (32 * kBlock);
+    const int col = tx & 31;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < 4; ++db) {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int d0 = db * 32 + 8 * rr + 4 * half_e;
-          u32x2 v2;
-          v2[0] = pack_bf16x2(ws.o[db][4 * rr] * inv, ws.o[db][4 * rr + 1] * inv);
-          v2[1] = pack_bf16x2(ws.o[db][4 * rr + 2] * inv, ws.o[db][4 * rr + 3] * inv);
-          *reinterpret_cast<u32x2*>(dst + d0) = v2;
-        }
+      for (int rr = 0; rr < 4; ++rr) {
+        u32x2 v2;
+        v2[0] = pack_bf16x2(ws.o[db][4 * rr] * inv, ws.o[db][4 * rr + 1] * inv);
+        v2[1] = pack_bf16x2(ws.o[db][4 * rr + 2] * inv, ws.o[db][4 * rr + 3] * inv);
+        const int c = db * 4 + rr;
+        *reinterpret_cast<u32x2*>(stage + col * kBlock + ((c ^ (col & 15)) << 3) + 4 * half_e) = v2;
       }
     }
-    if (a.lse && half_e == 0)
-      a.lse[b * a.ls_b + qrow * a.ls_s + h * a.ls_h] = any ? ws.m * kLn2 + logf(l) : -INFINITY;
+    const int lane = tx & 63;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 4 * i + (lane >> 4), c = lane & 15;
+      const u32x4 v4 = *reinterpret_cast<const u32x4*>(stage + r * kBlock + ((c ^ (r & 15)) << 3));
+      const int64_t row = (int64_t)t * kBlock + wq * 32 + r;
+      if (live && row < a.seq)
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + b * a.os_b + row * a.os_s +
+                                  h * a.os_h + c * 8) = v4;
+    }
   }
+  if (live && qrow < a.seq && a.lse && half_e == 0)
+    a.lse[b * a.ls_b + qrow * a.ls_s + h * a.ls_h] = any ? ws.m * kLn2 + logf(l) : -INFINITY;
 }
 
 // ---------------------------------------------------------------- merge
