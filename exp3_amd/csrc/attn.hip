@@ -168,6 +168,23 @@ __device__ __forceinline__ void dma_part(const uint16_t* src, uint16_t* lds, int
       : "memory");
 }
 
+// Per-lane gather into LDS: 16 bytes from this lane's own address land at
+// lds_wave + 16 x lane, lds_wave being the same for the whole wave. Issued from
+// assembly like dma_part, and awaited explicitly.
+__device__ __forceinline__ void dma_gather16(const void* src, uint32_t lds_wave) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_wave);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m0), "v"(src)
+      : "memory");
+}
+
 // threadIdx.x behind an opaque copy: values derived from it are recomputed for
 // every work item of a persistent workgroup instead of being held across items.
 __device__ __forceinline__ int thread_x() { return opaque((int)threadIdx.x); }
@@ -635,6 +652,28 @@ __device__ __forceinline__ void tail_item(const AttnArgs& a, int kd, int& pair, 
   pair = tpk * bg + rem / a.group;
 }
 
+// Q of a tile pair staged in LDS buffer 1 (tile t in K, tile t - 1 in V; 16-byte
+// chunk c of row r at r * 16 + (c ^ (r & 15))): whole 256-byte rows per 16 lanes,
+// so each copy instruction reads 8 full cache lines (loaded directly in the operand
+// layout, each instruction would read 32 bytes of each of 32 rows).
+__device__ __forceinline__ int q_stage_chunk(int row, int c) { return row * 16 + (c ^ (row & 15)); }
+
+__device__ __forceinline__ void copy_q(const AttnArgs& a, int b, int h, int t0, uint16_t* k1,
+                                       uint16_t* v1, int tid) {
+  const int w = tid >> 6;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int it = i >> 2;
+    const int e = (i & 3) * kAttnThreads + tid;
+    const int r = e >> 4, cs = e & 15;
+    const int t = t0 - it;
+    int64_t qrow = (int64_t)t * kBlock + r;
+    if (t < 0 || qrow >= a.seq) qrow = 0;   // a row that exists; its queries are not stored
+    const uint16_t* src = a.q + b * a.qs_b + qrow * a.qs_s + h * a.qs_h + ((cs ^ (r & 15)) << 3);
+    dma_gather16(src, lds_address(it ? v1 : k1) + (uint32_t)(((i & 3) * kAttnThreads + w * 64) * 16));
+  }
+}
+
 template <bool EXACT, bool TAIL, bool OUT_F32>
 __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg);
 
@@ -718,20 +757,9 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
   const int t = t_item[item];                        // may be -1 (odd tile count)
   const bool live = t >= 0;
 
+  copy_q(a, b, h, t_item[0], kbuf[1], vbuf[1], tid);   // read after the list phase
   WaveState ws;
   {
-    const int64_t qrow = (int64_t)t * kBlock + q_pos;
-    const uint16_t* src = a.q + b * a.qs_b + qrow * a.qs_s + h * a.qs_h + half * 8;
-    const bool ok = live && qrow < a.seq;
-#pragma unroll
-    for (int dc = 0; dc < 8; ++dc) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (ok) raw = *reinterpret_cast<const u32x4*>(src + dc * 16);
-      // consume the load here: the tile copies issued later share its counter,
-      // and a first use inside the block loop would wait for them every block
-      asm volatile("" : "+v"(raw));
-      ws.qb[dc] = as_bf16x8(raw);
-    }
     ws.m = -INFINITY;
     ws.l = 0.0f;
     ws.neg_m = 0.0f;
@@ -759,7 +787,14 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
       for (int j = tid; j <= tt; j += kAttnThreads) atomicAdd(&mult[it][j >> 1], 1u << ((j & 1) * 16));
     }
   }
+  wait_tiles();   // this wave's share of the Q copy (visible to all after the barrier)
   block_sync();
+  {
+    const uint16_t* qs = item ? vbuf[1] : kbuf[1];
+#pragma unroll
+    for (int dc = 0; dc < 8; ++dc)
+      ws.qb[dc] = as_bf16x8(*reinterpret_cast<const u32x4*>(qs + q_stage_chunk(q_pos, 2 * dc + half) * 8));
+  }
   // Processing order: every listed block except the two diagonal ones (t, t - 1),
   // ascending, then the diagonal ones. The block loop for the first part has a
   // single (unmasked) code path, which keeps O in one register set.
