@@ -641,6 +641,11 @@ __device__ __forceinline__ void static_item(const AttnArgs& a, int xcd, int loca
   }
 }
 
+// Work-queue counters: [0] the shared tail (one stream per XCD or fewer XCDs than
+// streams), [1 + x] XCD x's share of the static deal, [kStreamCounter0 + s] the
+// tail of stream s (8 / (B * Hkv) XCDs per stream, so at most 4 streams).
+constexpr int kStreamCounter0 = 9;
+
 // Item decode, shared tail: item kd of tile pairs static_tp.., (tile pair, stream,
 // head) heaviest first.
 __device__ __forceinline__ void tail_item(const AttnArgs& a, int kd, int& pair, int& hg) {
@@ -688,6 +693,10 @@ template <bool EXACT, bool TAIL, bool OUT_F32>
 __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs args) {
   const int xcd = blockIdx.x & 7;
   __shared__ int next_item;
+  // thread 0's draw state, kept in LDS so that no register holds it across items:
+  // this XCD's share used up; streams of the tail tried
+  __shared__ int share_done, steal;
+  if (threadIdx.x == 0) share_done = steal = 0;
   for (int round = 0;; ++round) {
     // The arguments are read afresh for every item through an opaque pointer, so
     // nothing derived from them is held in registers across items.
@@ -708,17 +717,49 @@ __global__ __launch_bounds__(kAttnThreads, 1) void attn_kernel(AttnArgs args) {
       const int n_static = a.xcds_per_stream > 1
           ? a.static_tp * a.group / a.xcds_per_stream
           : max(0, (a.static_tp * bg - xcd + 7) / 8) * a.group;
+      // With 8 / bg XCDs per stream, the tail is drawn per stream: a workgroup takes
+      // its own stream's light items first (their K / V tiles are in its L2), then
+      // those of the other streams once its own are gone.
+      const bool per_stream = a.xcds_per_stream > 1;
+      const int stream_items = (a.blocks + 1) / 2 - a.static_tp;   // tile pairs ..
+      const int per_stream_items = stream_items * a.group;        // .. x heads
       if (threadIdx.x == 0) {
-        int k = atomicAdd(a.queue + 1 + xcd, 1);
-        if (k >= n_static) k = n_static + atomicAdd(a.queue, 1);
-        next_item = k;
+        int k = -1;
+        if (!share_done) {
+          const int d = atomicAdd(a.queue + 1 + xcd, 1);
+          if (d < n_static) k = d;
+          else share_done = 1;
+        }
+        if (k < 0 && per_stream) {
+          for (; steal < bg; ++steal) {
+            const int st = (xcd + steal) % bg;
+            const int d = atomicAdd(a.queue + kStreamCounter0 + st, 1);
+            if (d < per_stream_items) {
+              k = n_static + st * per_stream_items + d;
+              break;
+            }
+          }
+        } else if (k < 0) {
+          const int d = atomicAdd(a.queue, 1);
+          if (d < a.dyn_items) k = n_static + d;
+        }
+        next_item = k;   // -1: no items left
       }
       block_sync();
       const int k = next_item;
       block_sync();  // read by every wave before thread 0 takes the next one
-      if (k < n_static) static_item(a, xcd, k, pair, hg);
-      else if (k - n_static < a.dyn_items) tail_item(a, k - n_static, pair, hg);
-      else break;
+      if (k < 0) break;
+      if (k < n_static) {
+        static_item(a, xcd, k, pair, hg);
+      } else if (per_stream) {
+        const int st = (k - n_static) / per_stream_items;
+        const int d = (k - n_static) - st * per_stream_items;
+        const int tpk = a.static_tp + d / a.group;
+        hg = d - (tpk - a.static_tp) * a.group;
+        pair = tpk * bg + st;
+      } else {
+        tail_item(a, k - n_static, pair, hg);
+      }
     }
     attn_item<EXACT, TAIL, OUT_F32>(a, pair, hg);
   }

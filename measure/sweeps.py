@@ -179,12 +179,12 @@ def run_pair_overlap(seq, seed, qk_scale, alpha):
 
     def timed(i, c, n=10):
         for _ in range(3):
-            b._attention(q, k, tiles, i, c, scale, None)
+            b._attention(q, k, tiles, i, c, scale, None, want_lse=False)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(n):
-            b._attention(q, k, tiles, i, c, scale, None)
+            b._attention(q, k, tiles, i, c, scale, None, want_lse=False)
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
@@ -219,12 +219,12 @@ def run_pair_overlap(seq, seed, qk_scale, alpha):
 def _attention_timer(torch, backend, q, k, tiles, scale):
     def timed(indices, counts, n=10):
         for _ in range(3):
-            backend._attention(q, k, tiles, indices, counts, scale, None)
+            backend._attention(q, k, tiles, indices, counts, scale, None, want_lse=False)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(n):
-            backend._attention(q, k, tiles, indices, counts, scale, None)
+            backend._attention(q, k, tiles, indices, counts, scale, None, want_lse=False)
         e1.record()
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n

@@ -1,13 +1,14 @@
 """The attention kernel's work queue (work_queue): with it the d = 128 kernel runs a
 persistent grid, one workgroup per CU taking (tile pair, head) items in turn: the
 first two thirds of the tile pairs from its own XCD's counter in the static deal's
-order, the light last third from one shared counter. Results must be bit-identical
-to the one-item-per-workgroup grid (the same items, each computed by one workgroup
-with the same arithmetic), and every item must be taken exactly once: each loop
-round of a workgroup draws once from its XCD's counter and, once that share is
-used up, once from the shared counter, so the counters end at the item counts
-plus one failed draw per workgroup. The d = 256 kernel deals its last third of tile
-ranks through the shared counter with 1.25 x as many tail workgroups as items."""
+order, then the light last third: per (batch, kv group) stream when several XCDs
+serve each stream (a workgroup drains its own stream's tail, then the others'), from
+one shared counter otherwise. Results must be bit-identical to the
+one-item-per-workgroup grid (the same items, each computed by one workgroup with the
+same arithmetic), and every item must be taken exactly once: each counter ends at
+its item count plus one failed draw per workgroup. The d = 256 kernel deals its last
+third of tile ranks through the shared counter with 1.25 x as many tail workgroups
+as items."""
 
 import numpy as np
 import pytest
@@ -85,6 +86,11 @@ def test_dynamic_tail_matches_static_schedule(gpu, layout, entry):
         static_items = sum(max(0, (tp0 * streams - x + 7) // 8) * group for x in range(8))
     tail_items = (np_ - tp0) * streams * group
     assert static_items + tail_items == np_ * streams * group
-    assert counters[0] == tail_items + grid
-    assert counters[1:9].sum() == static_items + tail_items + grid
-    assert not counters[9:].any()
+    assert counters[1:9].sum() == static_items + grid
+    if xps > 1:   # one tail counter per stream (from index 9), each tried by every workgroup
+        assert counters[0] == 0
+        assert (counters[9:9 + streams] == (np_ - tp0) * group + grid).all()
+        assert not counters[9 + streams:].any()
+    else:
+        assert counters[0] == tail_items + grid
+        assert not counters[9:].any()
