@@ -49,6 +49,7 @@ namespace spx {
 constexpr int kAttnThreads = 512;     // 8 waves: two query tiles x 4 waves x 32 rows
 constexpr int kItemWaves = 4;        // waves per query tile
 constexpr int kMaxBlocksAttn = 1024;
+constexpr int kListLoads = kMaxBlocksAttn / kAttnThreads;  // list positions per thread
 constexpr int kTailTile = 64;        // mean keys per tail tile (hi and lo rows fill K LDS)
 // log2 headroom before a column's running max moves. P is bf16 and O, l are fp32, all
 // with an 8-bit exponent, so probabilities up to 2^64 lose nothing; O then keeps
@@ -799,6 +800,22 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
   const bool live = t >= 0;
 
   copy_q(a, b, h, t_item[0], kbuf[1], vbuf[1], tid);   // read after the list phase
+  // Both items' list counts and entries are loaded now, with the Q copy in flight: every
+  // position a list row holds (NB) is read (rows and positions clamped into range, so
+  // no branch separates the loads), and those at or past the count are dropped.
+  int count_of[2] = {0, 0};
+  int64_t entry[2][kListLoads];
+  if (a.idx) {
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      const int tt = max(t_item[it], 0);
+      count_of[it] = a.cnt[b * a.cs_b + tt * a.cs_t + h * a.cs_h];
+      const int64_t* list = a.idx + b * a.is_b + tt * a.is_t + h * a.is_h;
+#pragma unroll
+      for (int r = 0; r < kListLoads; ++r)
+        entry[it][r] = list[min(tid + r * kAttnThreads, a.blocks - 1) * a.is_p];
+    }
+  }
   WaveState ws;
   {
     ws.m = -INFINITY;
@@ -817,12 +834,12 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
     const int tt = t_item[it];
     if (tt < 0) continue;
     if (a.idx) {
-      int count = a.cnt[b * a.cs_b + tt * a.cs_t + h * a.cs_h];
-      count = min(max(count, 0), a.blocks);
-      const int64_t* list = a.idx + b * a.is_b + tt * a.is_t + h * a.is_h;
-      for (int pos = tid; pos < count; pos += kAttnThreads) {
-        const int64_t j = list[pos * a.is_p];   // range-checked before narrowing
-        if (j >= 0 && j < a.blocks) atomicAdd(&mult[it][j >> 1], 1u << ((j & 1) * 16));
+      const int count = min(max(count_of[it], 0), a.blocks);   // tt >= 0 here
+#pragma unroll
+      for (int r = 0; r < kListLoads; ++r) {
+        const int64_t j = entry[it][r];   // range-checked before narrowing
+        if (tid + r * kAttnThreads < count && j >= 0 && j < a.blocks)
+          atomicAdd(&mult[it][j >> 1], 1u << ((j & 1) * 16));
       }
     } else {
       for (int j = tid; j <= tt; j += kAttnThreads) atomicAdd(&mult[it][j >> 1], 1u << ((j & 1) * 16));
