@@ -860,38 +860,49 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
     return (int)((mult[it][j >> 1] >> ((j & 1) * 16)) & 0xffffu);
   };
   int nu = 0;
-  auto compact = [&](bool diagonal_pass) {
-    for (int j0 = 0; j0 < a.blocks; j0 += kAttnThreads) {
-      const int j = j0 + tid;
-      int c0 = 0, c1 = 0;
-      if (j < a.blocks && ((j == t_item[0] || j == t_item[1]) == diagonal_pass)) {
-        c0 = times_listed(0, j);
-        c1 = times_listed(1, j);
-      }
-      const int e = max(c0, c1);   // occurrences of block j in the union
-      int incl = e;                // inclusive prefix sum over the wave
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int v = __shfl_up(incl, d);
-        if (lane >= d) incl += v;
-      }
-      if (lane == 63) wave_counts[w] = incl;
-      block_sync();
-      int offset = nu + incl - e;
-      for (int x = 0; x < w; ++x) offset += wave_counts[x];
-      for (int k = 0; k < e; ++k) {
-        ulist[offset + k] = (int16_t)j;
-        uflag[offset + k] = (uint8_t)((c0 > k ? 1 : 0) | (c1 > k ? 2 : 0));
-      }
-      for (int x = 0; x < kAttnThreads / 64; ++x) nu += wave_counts[x];
-      block_sync();
+  for (int j0 = 0; j0 < a.blocks; j0 += kAttnThreads) {
+    const int j = j0 + tid;
+    int c0 = 0, c1 = 0;
+    if (j < a.blocks && j != t_item[0] && j != t_item[1]) {
+      c0 = times_listed(0, j);
+      c1 = times_listed(1, j);
     }
-  };
-  compact(false);
+    const int e = max(c0, c1);   // occurrences of block j in the union
+    int incl = e;                // inclusive prefix sum over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int v = __shfl_up(incl, d);
+      if (lane >= d) incl += v;
+    }
+    if (lane == 63) wave_counts[w] = incl;
+    block_sync();
+    int offset = nu + incl - e;
+    for (int x = 0; x < w; ++x) offset += wave_counts[x];
+    for (int k = 0; k < e; ++k) {
+      ulist[offset + k] = (int16_t)j;
+      uflag[offset + k] = (uint8_t)((c0 > k ? 1 : 0) | (c1 > k ? 2 : 0));
+    }
+    for (int x = 0; x < kAttnThreads / 64; ++x) nu += wave_counts[x];
+    block_sync();
+  }
   const int n_full = __builtin_amdgcn_readfirstlane(nu);
-  compact(true);
-  nu = __builtin_amdgcn_readfirstlane(nu);
-
+  // the diagonal blocks t - 1, t (known ids) go after the others, ascending
+  if (tid == 0) {
+    int n = nu;
+#pragma unroll
+    for (int i = 1; i >= 0; --i) {
+      const int j = t_item[i];
+      if (j < 0) continue;
+      const int c0 = times_listed(0, j), c1 = times_listed(1, j);
+      for (int k = 0; k < max(c0, c1); ++k, ++n) {
+        ulist[n] = (int16_t)j;
+        uflag[n] = (uint8_t)((c0 > k ? 1 : 0) | (c1 > k ? 2 : 0));
+      }
+    }
+    wave_counts[0] = n;
+  }
+  block_sync();
+  nu = __builtin_amdgcn_readfirstlane(wave_counts[0]);
   if (EXACT && nu > 0) {
     const int64_t tile_elems = (int64_t)kBlock * kHeadDim;
     const uint16_t* kbase = a.kt + (((int64_t)b * a.kv_heads + g) * a.blocks) * tile_elems;
