@@ -415,8 +415,8 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
 
   l += __shfl_xor(l, 32);
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  if (row_ok) {
-    if (OUT_F32) {
+  if (OUT_F32) {
+    if (row_ok) {
       float* dst = static_cast<float*>(a.out) + b * a.os_b + qrow * a.os_s + h * a.os_h + 4 * half;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
@@ -427,25 +427,44 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
               f32x4{o[dt][r] * inv, o[dt][r + 1] * inv, o[dt][r + 2] * inv, o[dt][r + 3] * inv};
         }
       }
-    } else {
-      uint16_t* dst =
-          static_cast<uint16_t*>(a.out) + b * a.os_b + qrow * a.os_s + h * a.os_h + 4 * half;
+    }
+  } else {
+    // Each lane holds 4-dim pieces of its query row, so stored directly every store
+    // instruction would write 16 bytes into each of 32 rows. The wave stages its
+    // 32 x 256 bf16 rows in one of the (now free) K / V buffers, 16-byte chunk c of
+    // row r at c ^ (r & 31), and stores whole 512-byte rows, 32 lanes per row.
+    block_sync();   // every wave is done with the K / V buffers
+    // lane values re-derived here, so that nothing computed from them is hoisted
+    // above the block loops and held there
+    const int tx = opaque((int)threadIdx.x);
+    const int wv = __builtin_amdgcn_readfirstlane(tx >> 6);
+    const int lane_e = tx & 63, col_e = tx & 31, half_e = (tx >> 5) & 1;
+    uint16_t* stage = wv < 2 ? kbuf[wv] : vbuf[wv - 2];
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
+    for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
-        for (int grp = 0; grp < 4; ++grp) {
-          const int r = 4 * grp;
-          u32x2 v;
-          v[0] = pack_bf16x2(o[dt][r] * inv, o[dt][r + 1] * inv);
-          v[1] = pack_bf16x2(o[dt][r + 2] * inv, o[dt][r + 3] * inv);
-          *reinterpret_cast<u32x2*>(dst + dt * 32 + 8 * grp) = v;
-        }
+      for (int grp = 0; grp < 4; ++grp) {
+        const int r = 4 * grp;
+        u32x2 v;
+        v[0] = pack_bf16x2(o[dt][r] * inv, o[dt][r + 1] * inv);
+        v[1] = pack_bf16x2(o[dt][r + 2] * inv, o[dt][r + 3] * inv);
+        const int c = dt * 4 + grp;
+        *reinterpret_cast<u32x2*>(stage + col_e * kD2 + ((c ^ col_e) << 3) + 4 * half_e) = v;
       }
     }
-    if (a.lse && half == 0)
-      a.lse[b * a.ls_b + qrow * a.ls_s + h * a.ls_h] =
-          l > 0.0f ? (log2f(l) - neg_m) * kLn2 : -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = 2 * i + (lane_e >> 5), c = lane_e & 31;
+      const u32x4 v4 = *reinterpret_cast<const u32x4*>(stage + r * kD2 + ((c ^ r) << 3));
+      const int64_t row = (int64_t)t * kBlock + wv * 32 + r;
+      if (row < a.seq)
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + b * a.os_b + row * a.os_s +
+                                  h * a.os_h + c * 8) = v4;
+    }
   }
+  if (row_ok && a.lse && half == 0)
+    a.lse[b * a.ls_b + qrow * a.ls_s + h * a.ls_h] =
+        l > 0.0f ? (log2f(l) - neg_m) * kLn2 : -INFINITY;
 }
 
 int launch_attention_256(const Attn256Options& opt, const void* q, const int64_t* q_strides,
