@@ -11,9 +11,12 @@
 // Row i of tile t is valid for block j iff i >= 128 (j + 1) - 1 and i < S. Each
 // lane reduces its 16 rows of one block column to (max, sum 2^(x - max)); the
 // eight partials of a chunk (4 waves x 2 lane halves) are merged in a fixed order
-// after the next chunk's barrier, giving M_tj and m_tj. One wave then runs the
-// normalisation w_j = m_tj 2^(M_tj - max_j M_tj) / (sum_j w + 1e-9) and the
-// selection of the row, so the raw scores never reach HBM.
+// after the next chunk's barrier, giving M_tj and m_tj. The normalisation
+// w_j = m_tj 2^(M_tj - max_j M_tj) / (sum_j w + 1e-9) and the selection then run
+// on the row held by one wave, so the raw scores never reach HBM: for the routed
+// lists, a second kernel with one workgroup per (b, t) takes every head's row
+// (M, m) from the tile's index slab, where the first kernel left them, and writes
+// the slab's lists and mask in whole cache lines.
 //
 // Selection (upstream :357-407 and kernels.py:129-160) is one shared device
 // routine over a score row held in LDS: threshold fp32(max * alpha), protected
@@ -160,44 +163,70 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 
 // V1 selection (upstream :357-407 with min_budget = 0) of one normalised score row
 // held in registers by one wave (block c * 64 + lane in sv[c]): the same rule as
-// select_row, compacted 64 key blocks per ballot.
+// select_row, one ballot per 64 key blocks. Bit lane of words[c] says whether
+// block c * 64 + lane is selected (c < ceil(kb / 64)); returns the count.
 constexpr int kRowChunks = kMaxBlocks / 64;
-__device__ __forceinline__ void select_v1_row_regs(const float (&sv)[kRowChunks], int t,
-                                                   const SelectParams& p, const SelectOut& o) {
+template <int NC>
+__device__ __forceinline__ int select_v1_row_bits(const float (&sv)[NC], int t,
+                                                  const SelectParams& p, uint64_t* words) {
   const int lane = threadIdx.x & 63;
   const int kb = p.key_blocks;
   const int nch = (kb + 63) >> 6;
+  // per-lane conditions are selects, not branches (the chunk test is uniform)
   float local = -INFINITY;
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c)
-    if (c < nch && c * 64 + lane < kb) local = max_nan(local, sv[c]);
+  for (int c = 0; c < NC; ++c)
+    if (c < nch) local = max_nan(local, c * 64 + lane < kb ? sv[c] : -INFINITY);
   const float maximum = wave_max_dpp(local);
   const float threshold = maximum * p.alpha;   // fp32(max * fp32(alpha))
   const bool last_rows = t >= p.query_blocks - p.last;
-  int base = 0;
+  int count = 0;
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
+  for (int c = 0; c < NC; ++c) {
     if (c < nch) {   // wave-uniform
       const int j = c * 64 + lane;
-      bool active = false;
-      if (j < kb) {
-        const bool keep = sv[c] >= threshold;
-        const int distance = t - j;
-        const bool prot = j < p.sink || (distance >= 0 && distance < p.window) || last_rows;
-        active = (keep || prot) && distance >= 0;
-        if (o.mask) o.mask[o.row_base + (int64_t)j * o.heads] = active ? 1 : 0;
-      }
+      const bool keep = sv[c] >= threshold;
+      const int distance = t - j;
+      const bool prot = j < p.sink || (distance >= 0 && distance < p.window) || last_rows;
+      const bool active = j < kb && (keep || prot) && distance >= 0;
       const uint64_t ballot = __ballot(active);
-      const int before = __popcll(ballot & ((1ull << lane) - 1ull));
-      if (active && o.indices) o.indices[o.row_base + (int64_t)(base + before) * o.heads] = j;
-      base += __popcll(ballot);
+      if (lane == 0) words[c] = ballot;
+      count += __popcll(ballot);
     }
   }
-  if (o.indices) {
-    for (int pos = base + lane; pos < kb; pos += 64)
-      o.indices[o.row_base + (int64_t)pos * o.heads] = kb;
+  return count;
+}
+
+// normalize_scores (upstream :410-417) of one score row held by one wave over
+// j <= t: block j = c * 64 + lane has running max mx[c] and mass ms[c] (mx -inf
+// when no row of the tile is valid for it); on return mx[c] holds its normalised
+// score w_j / (sum w + 1e-9), w_j = ms 2^(mx - max_j mx), and 0 beyond t. Chunks
+// c >= nch are left as they are.
+template <int NC>
+__device__ __forceinline__ void normalize_row_regs(float (&mx)[NC], const float (&ms)[NC], int t,
+                                                   int nch) {
+  // per-lane conditions are selects, not branches (the chunk test is uniform):
+  // fmaxf with -inf and sums with 0 leave the results unchanged
+  const int lane = threadIdx.x & 63;
+  float local = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+    if (c < nch) local = fmaxf(local, c * 64 + lane <= t ? mx[c] : -INFINITY);
+  const float gmax = wave_max_dpp(local);
+  float wsum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c < nch) {
+      const float e = ms[c] * exp2_fast(mx[c] - gmax);
+      const float w = (c * 64 + lane <= t && mx[c] != -INFINITY) ? e : 0.0f;
+      wsum += w;
+      mx[c] = w;
+    }
   }
-  if (o.counts && lane == 0) o.counts[o.count_off] = base;
+  const float total = wave_sum_dpp(wsum) + 1e-9f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+    if (c < nch) mx[c] = c * 64 + lane <= t ? mx[c] / total : 0.0f;
 }
 
 // ------------------------------------------------------------ V1 scores
@@ -261,15 +290,15 @@ __device__ __forceinline__ void chunk_column(const f32x16& acc, float c, int lim
   }
 }
 
-// Dynamic LDS of the V1 kernel: blk_max, blk_mass [NB].
+// Dynamic LDS of the V1 kernel when it normalises its own row: blk_max, blk_mass [NB].
 __host__ __device__ constexpr size_t v1_lds_bytes(int blocks) { return 2u * (size_t)blocks * 4u; }
 
-// Block-mean chunks (32 blocks x D dims bf16) stream through a ring of LDS slots,
-// each copied once per workgroup by direct global->LDS loads and read by all four
-// waves as MFMA B operands; kV1Ring - 1 chunks are in flight ahead of the one
-// being reduced.
-template <int D> struct V1Ring {
-  static constexpr int kSlots = D == 128 ? 4 : 3;
+// Block-mean chunks (32 blocks x D dims bf16) stream through a ring of S LDS
+// slots, each copied once per workgroup by direct global->LDS loads and read by all
+// four waves as MFMA B operands; S - 1 chunks are in flight ahead of the one being
+// reduced.
+template <int D, int S> struct V1Ring {
+  static constexpr int kSlots = S;
   static constexpr int kUnitsPerRow = D / 8;                  // 16-byte units of one block row
   static constexpr int kSlotElems = 32 * D;
   static constexpr int kCopiesPerWave = 32 * kUnitsPerRow / 64 / 4;   // D/64 loads per wave
@@ -301,9 +330,16 @@ template <int N> __device__ __forceinline__ void v1_wait_ring() {
 }
 __device__ __forceinline__ void v1_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-template <int D, bool kPosScale>
+// kSplit: the routed form. The workgroup leaves each block's (max, mass) for its
+// row in the index slab of its (b, t), the [NB, Hq] int64 entries the tile's
+// lists will occupy: float2 entry h * NB + j of the slab for block j <= t (row h
+// contiguous), and ends; v1_select_kernel then normalises and selects every row
+// of the tile and overwrites the slab with the lists, so this kernel's LDS is
+// not held through that epilogue. Otherwise (scores only) wave 0 normalises the
+// row from LDS and writes the scores.
+template <int D, int kSlots, bool kPosScale, bool kSplit>
 __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
-  using Ring = V1Ring<D>;
+  using Ring = V1Ring<D, kSlots>;
   constexpr int kSteps = D / 16;  // 16-dim MFMA k-steps
   constexpr int R = Ring::kSlots;
   // Workgroups go to the 8 XCDs round-robin by id: the k-th one on XCD x takes
@@ -329,6 +365,8 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   const int nb = a.blocks;
   float* blk_max = v1_lds;
   float* blk_mass = v1_lds + nb;
+  // kSplit: this row's partials in the slab of (b, t)
+  const int64_t part_base = (((int64_t)b * a.blocks + t) * a.blocks) * a.q_heads + (int64_t)h * a.blocks;
 
   // Slot image: 16-byte unit u of block row r at unit u ^ (r & 15), so that the
   // operand reads below (32 rows, one unit each) are free of bank conflicts. Lane
@@ -401,11 +439,12 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
     part_max[jc & 1][2 * wave + half][col] = mx;
     part_mass[jc & 1][2 * wave + half][col] = mass;
   };
-  // the eight partials (4 waves x 2 lane halves) of chunk jc -> blk_max / blk_mass,
-  // in a fixed order (threads 0..31)
+  // the eight partials (4 waves x 2 lane halves) of chunk jc -> the block's (max,
+  // mass), in a fixed order (threads 0..31): into blk_max / blk_mass, or (kSplit)
+  // into the row's index slots for j <= t
   auto merge_chunk = [&](int jc) {
     const int jj = jc * 32 + tid;
-    if (tid < 32 && jj < nb) {
+    if (tid < 32 && (kSplit ? jj <= t : jj < nb)) {
       float m = part_max[jc & 1][0][tid];
 #pragma unroll
       for (int w = 1; w < 8; ++w) m = fmaxf(m, part_max[jc & 1][w][tid]);
@@ -415,8 +454,12 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
         for (int w = 0; w < 8; ++w)
           s2 += part_mass[jc & 1][w][tid] * exp2_fast(part_max[jc & 1][w][tid] - m);
       }
-      blk_max[jj] = m;
-      blk_mass[jj] = s2;
+      if constexpr (kSplit) {
+        reinterpret_cast<float2*>(a.indices)[part_base + jj] = make_float2(m, s2);
+      } else {
+        blk_max[jj] = m;
+        blk_mass[jj] = s2;
+      }
     }
   };
   // Q is consumed here, so the compiler's wait for it (which also covers the
@@ -437,61 +480,124 @@ __global__ __launch_bounds__(kRouteThreads) void v1_route_kernel(V1Args a) {
   }
   block_sync();
   if (nchunks > 0) merge_chunk(nchunks - 1);
+  if constexpr (kSplit) return;
   block_sync();
-  // One wave finishes the row: normalisation and selection touch at most NB
-  // (<= 1024) entries, 16 per lane, and in one wave they need no barriers or
-  // cross-wave reductions; the other waves end here.
+  // Scores only: one wave normalises the row (at most NB <= 1024 entries, 16 per
+  // lane, held in registers: no barriers or cross-wave reductions); the other
+  // waves end here.
   if (wave != 0) return;
-
-  // normalize_scores over j <= t (j > t has M = -inf and contributes 0), on the row
-  // held in registers: lane holds blocks c * 64 + lane, loops fully unrolled
   const int nch = (a.blocks + 63) >> 6;
-  float sv[kRowChunks];
-  float local = -INFINITY;
+  float sv[kRowChunks], sm[kRowChunks];
 #pragma unroll
   for (int c = 0; c < kRowChunks; ++c) {
-    sv[c] = -INFINITY;   // the block's M, then its weight, then its score
-    if (c < nch) {
-      const int jj = c * 64 + lane;
-      if (jj <= t) {
-        sv[c] = blk_max[jj];
-        local = fmaxf(local, sv[c]);
+    sv[c] = -INFINITY;
+    sm[c] = 0.0f;
+    const int jj = c * 64 + lane;
+    if (c < nch && jj <= t) {
+      sv[c] = blk_max[jj];
+      sm[c] = blk_mass[jj];
+    }
+  }
+  normalize_row_regs(sv, sm, t, nch);
+#pragma unroll
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int jj = c * 64 + lane;
+    if (c < nch && jj < a.blocks) a.score[b * a.ss_b + t * a.ss_t + jj * a.ss_j + h * a.ss_h] = sv[c];
+  }
+}
+
+// Normalisation and selection of the routed rows (upstream :410-417 and
+// :357-407) from the per-block (max, mass) that v1_route_kernel<..., kSplit> left
+// in the index slab of each (b, t): one workgroup per (b, t), heaviest tiles
+// first. Each wave takes rows h = wave, wave + 16, ...: it loads the row's
+// partials (contiguous), normalises the row in registers and records its
+// selection as one ballot word per 64 key blocks in LDS. After the barrier every
+// partial has been read, and the tile's [NB, Hq] index and mask slabs are
+// written with consecutive lanes on consecutive entries (whole cache lines), in
+// passes over groups of heads whose lists fit the LDS list buffer (one pass
+// unless Hq * NB > 32768): the group's rows are compacted from their words into
+// LDS lists, then entry (p, h) is the p-th selected block of row h, or NB past
+// the row's count.
+constexpr int kSelectThreads = 1024;
+constexpr int kSelectMaxHeads = 256;
+constexpr int kSelectListEntries = 32768;   // uint16 list entries in LDS (64 KB)
+
+__host__ __device__ constexpr size_t v1_select_lds_bytes(int heads, int nc) {
+  return (size_t)heads * ((size_t)nc * 8 + 4) + (size_t)kSelectListEntries * 2;
+}
+
+template <int NC>   // NC >= ceil(NB / 64) chunks of 64 key blocks per row
+__global__ __launch_bounds__(kSelectThreads) void v1_select_kernel(V1Args a) {
+  extern __shared__ __align__(8) unsigned char sel_lds[];
+  const int H = a.q_heads, NB = a.blocks;
+  uint64_t* words = reinterpret_cast<uint64_t*>(sel_lds);          // [H][NC]
+  int* count = reinterpret_cast<int*>(words + (size_t)H * NC);     // [H]
+  uint16_t* list = reinterpret_cast<uint16_t*>(count + H);         // [group heads][NB]
+  const int b = (int)blockIdx.x % a.batch;
+  const int t = NB - 1 - (int)blockIdx.x / a.batch;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kWaves = kSelectThreads / 64;
+  const int64_t slab = (((int64_t)b * NB + t) * NB) * H;
+  const float2* part = reinterpret_cast<const float2*>(a.indices) + slab;
+  const int nch = (NB + 63) >> 6;
+  for (int h = wave; h < H; h += kWaves) {
+    float sv[NC], sm[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      sv[c] = -INFINITY;
+      sm[c] = 0.0f;
+      if (c < nch) {   // wave-uniform; lanes past t read entry t and drop it
+        const int jj = c * 64 + lane;
+        const float2 p = part[(int64_t)h * NB + min(jj, t)];
+        sv[c] = jj <= t ? p.x : -INFINITY;
+        sm[c] = jj <= t ? p.y : 0.0f;
       }
     }
-  }
-  const float gmax = wave_max_dpp(local);
-  float wsum = 0.0f;
+    normalize_row_regs(sv, sm, t, nch);
+    if (a.score) {
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    if (c < nch) {
-      const int jj = c * 64 + lane;
-      float w = 0.0f;
-      if (jj <= t) {
-        w = (sv[c] != -INFINITY) ? blk_mass[jj] * exp2_fast(sv[c] - gmax) : 0.0f;
-        wsum += w;
+      for (int c = 0; c < NC; ++c) {
+        const int jj = c * 64 + lane;
+        if (c < nch && jj < NB) a.score[b * a.ss_b + t * a.ss_t + jj * a.ss_j + h * a.ss_h] = sv[c];
       }
-      sv[c] = w;
     }
+    const int n = select_v1_row_bits(sv, t, a.sel, words + (size_t)h * NC);
+    if (lane == 0) count[h] = n;
   }
-  const float total = wave_sum_dpp(wsum) + 1e-9f;
+  block_sync();   // every partial of the slab has been read
+  if (tid < H) a.counts[((int64_t)b * NB + t) * H + tid] = count[tid];
+  const int group = min(H, kSelectListEntries / NB);   // >= 32 (NB <= 1024)
+  const int span = kSelectThreads / group;              // positions per sweep
+  const int p_off = tid / group, hl = tid - p_off * group;
+  for (int h0 = 0; h0 < H; h0 += group) {
+    const int gh = min(group, H - h0);
+    // lists of the group's rows, compacted from their words
+    for (int r = wave; r < gh; r += kWaves) {
+      const uint64_t* w = words + (size_t)(h0 + r) * NC;
+      int base = 0;
 #pragma unroll
-  for (int c = 0; c < kRowChunks; ++c) {
-    if (c < nch) {
-      const int jj = c * 64 + lane;
-      const float sc = jj <= t ? sv[c] / total : 0.0f;
-      sv[c] = sc;
-      if (a.score && jj < a.blocks) a.score[b * a.ss_b + t * a.ss_t + jj * a.ss_j + h * a.ss_h] = sc;
+      for (int c = 0; c < NC; ++c) {
+        if (c < nch) {
+          const uint64_t m = w[c];
+          if ((m >> lane) & 1ull)
+            list[r * NB + base + __popcll(m & ((1ull << lane) - 1ull))] = (uint16_t)(c * 64 + lane);
+          base += __popcll(m);
+        }
+      }
     }
-  }
-  if (a.indices) {
-    SelectOut o;
-    o.indices = a.indices;
-    o.counts = a.counts;
-    o.mask = a.mask;
-    o.heads = a.q_heads;
-    o.row_base = (((int64_t)b * a.blocks + t) * a.blocks) * a.q_heads + h;
-    o.count_off = ((int64_t)b * a.blocks + t) * a.q_heads + h;
-    select_v1_row_regs(sv, t, a.sel, o);
+    block_sync();
+    if (p_off < span && hl < gh) {
+      const int h = h0 + hl;
+      const int n = count[h];
+      for (int p = p_off; p < NB; p += span)
+        a.indices[slab + (int64_t)p * H + h] = p < n ? (int64_t)list[hl * NB + p] : (int64_t)NB;
+      if (a.mask) {
+        const uint64_t* w = words + (size_t)h * NC;
+        for (int j = p_off; j < NB; j += span)
+          a.mask[slab + (int64_t)j * H + h] = (uint8_t)((w[j >> 6] >> (j & 63)) & 1ull);
+      }
+    }
+    block_sync();   // the list buffer is free for the next group
   }
 }
 
@@ -628,20 +734,40 @@ static int v1_common(const void* q, const int64_t* q_strides, const void* mean_k
 }
 
 // One workgroup per (query tile, batch, q head), the tile count padded to a
-// multiple of 8 (the XCD count); LDS sized to the block count (at most 40 KB at
-// 1024 blocks). A positive scale takes the row maxima over the raw products; any
-// other scale (zero, negative, NaN) scales every product first.
+// multiple of 8 (the XCD count). Scores only: LDS sized to the block count (at
+// most 40 KB at 1024 blocks), the row normalised in the same launch. Routed:
+// the select kernel follows on the same stream. A positive scale takes the row
+// maxima over the raw products; any other scale (zero, negative, NaN) scales
+// every product first.
+template <int D, int kSlots, bool kSplit>
+static void launch_v1_as(const V1Args& a, hipStream_t st) {
+  const int tiles8 = 8 * ((a.blocks + 7) / 8);
+  const int grid = tiles8 * a.batch * a.q_heads;
+  const size_t lds = kSplit ? 0 : v1_lds_bytes(a.blocks);
+  if (a.scale_log2 > 0.0f) v1_route_kernel<D, kSlots, true, kSplit><<<grid, kRouteThreads, lds, st>>>(a);
+  else v1_route_kernel<D, kSlots, false, kSplit><<<grid, kRouteThreads, lds, st>>>(a);
+  if (kSplit) {
+    const int nch = (a.blocks + 63) / 64;
+    const int grid = a.blocks * a.batch;
+    const int h = a.q_heads;
+    constexpr int T = kSelectThreads;
+    if (nch <= 1) v1_select_kernel<1><<<grid, T, v1_select_lds_bytes(h, 1), st>>>(a);
+    else if (nch <= 2) v1_select_kernel<2><<<grid, T, v1_select_lds_bytes(h, 2), st>>>(a);
+    else if (nch <= 4) v1_select_kernel<4><<<grid, T, v1_select_lds_bytes(h, 4), st>>>(a);
+    else if (nch <= 8) v1_select_kernel<8><<<grid, T, v1_select_lds_bytes(h, 8), st>>>(a);
+    else v1_select_kernel<16><<<grid, T, v1_select_lds_bytes(h, 16), st>>>(a);
+  }
+}
+
 static void launch_v1(const V1Args& a, int head_dim, void* stream) {
-  const int grid = 8 * ((a.blocks + 7) / 8) * a.batch * a.q_heads;
-  const size_t lds = v1_lds_bytes(a.blocks);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool pos = a.scale_log2 > 0.0f;
+  const bool split = a.indices != nullptr;
   if (head_dim == 128) {
-    if (pos) v1_route_kernel<128, true><<<grid, kRouteThreads, lds, st>>>(a);
-    else v1_route_kernel<128, false><<<grid, kRouteThreads, lds, st>>>(a);
+    if (split) launch_v1_as<128, 4, true>(a, st);
+    else launch_v1_as<128, 4, false>(a, st);
   } else {
-    if (pos) v1_route_kernel<256, true><<<grid, kRouteThreads, lds, st>>>(a);
-    else v1_route_kernel<256, false><<<grid, kRouteThreads, lds, st>>>(a);
+    if (split) launch_v1_as<256, 3, true>(a, st);
+    else launch_v1_as<256, 3, false>(a, st);
   }
 }
 
@@ -671,6 +797,10 @@ extern "C" int spx_v1_route(const void* q, const int64_t* q_strides, const void*
                     head_dim, block_size, scale, &a);
   if (e) return e;
   SPX_REQUIRE(indices && counts, SPX_EINVAL, "indices / counts: null pointer");
+  SPX_REQUIRE(q_heads <= kSelectMaxHeads, SPX_EUNSUPPORTED, "q_heads %d exceeds %d", q_heads,
+              kSelectMaxHeads);
+  SPX_REQUIRE((reinterpret_cast<uintptr_t>(indices) & 7) == 0, SPX_EINVAL,
+              "indices: base pointer must be 8-byte aligned");
   a.score = score;
   const int64_t nb = a.blocks;
   a.ss_h = 1; a.ss_j = q_heads; a.ss_t = nb * q_heads; a.ss_b = nb * nb * q_heads;

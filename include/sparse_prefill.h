@@ -125,9 +125,12 @@ int spx_protected_selection(const float* score, const int64_t* score_strides, in
                             int sink_blocks, int window_blocks, int last_full_blocks,
                             uint8_t* mask, int64_t* indices, int32_t* counts, void* stream);
 
-/* Fused V1 route: spx_v1_scores and spx_deal_output_score in one launch, the
- * selection reading the exact score values it writes. score may be NULL (not
- * stored); mask may be NULL. Replaces attention.py:87-105 (_v1_selection's
+/* Fused V1 route: spx_v1_scores and spx_deal_output_score without the scores
+ * passing through HBM, the selection reading the exact score values it writes
+ * (two kernels on `stream`: the block products leave per-block partials in each
+ * tile's own [KB, H] slab of `indices`, which the second overwrites with the
+ * lists). score may be NULL (not stored); mask may be NULL. q_heads <= 256;
+ * indices 8-byte aligned. Replaces attention.py:87-105 (_v1_selection's
  * selector + indices stages). */
 int spx_v1_route(const void* q, const int64_t* q_strides, const void* mean_k,
                  const int64_t* mean_k_strides, int batch, int seq, int q_heads,

@@ -128,6 +128,31 @@ def test_v1_route_non_positive_scale(gpu, scale):
     np.testing.assert_array_equal(to_np(cnt), e_cnt)
 
 
+def test_v1_route_head_groups(gpu):
+    """The routed form writes each tile's [NB, Hq] index and mask slabs from LDS
+    lists, in passes over groups of heads when Hq x NB exceeds its 32768-entry
+    list buffer: here 128 q heads x 258 blocks, two passes (127 heads, then 1).
+    The fused route's mask equals the selection rule on its own scores, and its
+    lists and counts equal that mask's. Inputs are drawn on the GPU (1 GB of Q)."""
+    length, q_heads, kv_heads, alpha = 258 * 128 - 100, 128, 8, 0.5
+    gen = torch.Generator(device="cuda").manual_seed(29)
+    q = (torch.randn(1, length, q_heads, 128, generator=gen, device="cuda") * 4).to(torch.bfloat16)
+    k = torch.randn(1, length, kv_heads, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn(1, length, kv_heads, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    backend = attention.AttentionBackend(alpha=alpha, register=False)
+    backend.configure("fp_v1", alpha)
+    record = {"events": {}}
+    _, _, scores, idx, cnt, sel = backend._v1_selection(q, k, SCALE, record, v, True)
+    del q, k, v
+    g_scores = to_np(scores)
+    assert g_scores.shape == (1, 258, 258, q_heads)
+    own = ref.mask_from_indices(*ref.deal_output_score(g_scores, 2, 4, alpha, 2, 0))
+    np.testing.assert_array_equal(to_np(sel), own)
+    e_idx, e_cnt = ref.indices_from_mask(own)
+    np.testing.assert_array_equal(to_np(cnt), e_cnt)
+    np.testing.assert_array_equal(to_np(idx), e_idx)
+
+
 def _adversarial_scores(length, seed):
     """Score tensors that stress the threshold: raised-to-the-4th V1 scores
     (check_math.py:305-311), exact ties with the threshold, zero rows."""
