@@ -33,6 +33,12 @@
       greedy dispatch to each XCD's CUs in grid order) under the shipped mapping
       and the earlier one-tile-pair-per-XCD mapping, with per-item costs from
       the cost model; also for the dense (all causal blocks) lists
+  python -m measure.sweeps route [--cases 32640:128:28,32640:256:16,131072:128:28]
+      the fused V1 route (spx_v1_route: block products, then the per-tile
+      normalisation and selection) on the seeded inputs, seq:head_dim:q_heads per
+      case with 4 KV heads, alpha 0.08: HIP events around 50 back-to-back calls
+      after 5 warm-up calls; microseconds per call and the rate over its
+      algorithmic bytes (Q read once, int64 indices and the mask written)
   python -m measure.sweeps model [--seq 32640] [--layers 28] [--repeats 3]
       full prefill of a random-init Qwen2.5-7B-shaped model built from a local
       config (28 layers, hidden 3584, FFN 18944, 28/4 heads, RMSNorm 1e-6,
@@ -229,6 +235,48 @@ def _attention_timer(torch, backend, q, k, tiles, scale):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
     return timed
+
+
+def run_route(cases, seed):
+    """spx_v1_route alone, per (seq, head_dim, q_heads) case (see the module docstring)."""
+    import torch
+    from exp3_amd import _lib, synthetic
+    from exp3_amd.upstream import flashprefill_native_forward as up
+    _lib.load()
+    for seq, head_dim, q_heads in cases:
+        q, k, _, _ = synthetic.make_inputs(seq, seed=seed, q_heads=q_heads, kv_heads=4,
+                                           head_dim=head_dim, device="cuda")
+        kbar = up.block_mean_k(k)
+        batch, _, heads, dim = q.shape
+        blocks = kbar.shape[1]
+        idx = torch.empty(batch, blocks, blocks, heads, dtype=torch.int64, device="cuda")
+        cnt = torch.empty(batch, blocks, heads, dtype=torch.int32, device="cuda")
+        sel = torch.empty(batch, blocks, blocks, heads, dtype=torch.bool, device="cuda")
+
+        def route():
+            _lib.call("spx_v1_route", _lib.ptr(q), _lib.strides(q), _lib.ptr(kbar),
+                      _lib.strides(kbar), batch, seq, heads, k.shape[2], dim, 128,
+                      dim ** -0.5, 0.08, 2, 4, 2, None, _lib.ptr(idx), _lib.ptr(cnt),
+                      _lib.ptr(sel), _lib.stream(q.device))
+
+        for _ in range(5):
+            route()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        reps = 50
+        e0.record()
+        for _ in range(reps):
+            route()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1e3
+        nbytes = q.numel() * 2 + idx.numel() * 9 + cnt.numel() * 4
+        print(json.dumps({"sweep": "route", "seq": seq, "head_dim": head_dim, "q_heads": q_heads,
+                          "us": round(us, 1), "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                          "frac_hbm": round(nbytes / (us * 1e-6) / 8e12, 3)}), flush=True)
+        del q, k, kbar, idx, cnt, sel
+        torch.cuda.empty_cache()
 
 
 def run_cost_model(seq, seed):
@@ -572,6 +620,9 @@ def main(argv=None) -> int:
     xb.add_argument("--alpha", type=float, default=0.7)
     xb.add_argument("--costs", default="12.6,3.45,2.02",
                     help="microseconds per CU: fixed per workgroup, shared step, one-sided step")
+    ro = sub.add_parser("route")
+    ro.add_argument("--cases", default="32640:128:28,32640:256:16,131072:128:28")
+    ro.add_argument("--seed", type=int, default=17)
     mo = sub.add_parser("model")
     mo.add_argument("--seq", type=int, default=32640)
     mo.add_argument("--layers", type=int, default=28)
@@ -592,6 +643,8 @@ def main(argv=None) -> int:
         run_d256(args.seq, args.seed)
     elif args.cmd == "pair-overlap":
         run_pair_overlap(args.seq, args.seed, args.qk_scale, args.alpha)
+    elif args.cmd == "route":
+        run_route([tuple(int(x) for x in c.split(":")) for c in args.cases.split(",")], args.seed)
     elif args.cmd == "cost-model":
         run_cost_model(args.seq, args.seed)
     elif args.cmd == "xcd-balance":
