@@ -13,7 +13,10 @@
 //
 // Bandwidth-bound: each workgroup streams a 128 x D bf16 K tile and V tile with
 // 16-byte loads (each row is 2 D contiguous bytes), reduces columns in registers,
-// across lanes and across the four waves through LDS.
+// across lanes and across the four waves through LDS. The V transpose stages one
+// 64-key half of the rows in LDS at a time (the value slot permutation keeps slots
+// 0-63 on keys 0-63), 25 KB of LDS per workgroup at D = 128: four workgroups per
+// CU, so a 32K-token layer's 1020 workgroups run in one round.
 //
 // Head dim 256 (Qwen3.5 full-attention layers): the same pass; key tiles keep the
 // [128 keys][256 dims] layout (chunk c of row r at c ^ (r & 15), c < 32), value tiles
@@ -79,13 +82,14 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
   const int n = min(kBlock, a.seq - j * kBlock);
 
   __shared__ float part[4][4][D];                          // [quantity][wave][dim]
-  __shared__ __align__(16) uint16_t vrows[kBlock * kVPitch];  // staged V rows
+  __shared__ __align__(16) uint16_t vrows[kBlock / 2 * kVPitch];  // staged V rows, one half at a time
   __shared__ float sig_part[D / 64];
 
   float sk[8] = {}, qk[8] = {}, sv[8] = {}, qv[8] = {};
   const uint16_t* kbase = a.k + b * a.ks_b + g * a.ks_h + (int64_t)c * 8;
   const uint16_t* vbase = a.v + b * a.vs_b + g * a.vs_h + (int64_t)c * 8;
   const int64_t tile_off = ((((int64_t)b * a.kv_heads + g) * a.blocks + j) * kBlock) * D;
+  u32x4 vraw[kRowsPer];   // this thread's V rows (all in one half of the block)
 
 #pragma unroll
   for (int i = 0; i < kRowsPer; ++i) {
@@ -103,11 +107,7 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (valid) raw = *reinterpret_cast<const u32x4*>(vbase + token * a.vs_s);
       if (DO_V && valid) accumulate8(raw, sv, qv);
-      if (DO_TILES) {
-        uint32_t* dst = reinterpret_cast<uint32_t*>(vrows + row * kVPitch + c * 8);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[e] = raw[e];
-      }
+      if (DO_TILES) vraw[i] = raw;
     }
   }
 
@@ -155,28 +155,43 @@ __global__ __launch_bounds__(kPoolThreads) void pool_kernel(PoolArgs a) {
     // chunk position (D = 128: [dim][128 slots], chunk gc ^ (d & 15); D = 256: sub-block
     // gc / 4 of [dim][32 slots], chunk (gc & 3) ^ ((d >> 2) & 3)).
     uint16_t* tile = a.value_tiles + tile_off;
+    const int my_half = rg * kRowsPer / (kBlock / 2);
 #pragma unroll
-    for (int i = 0; i < 16 * D / kPoolThreads; ++i) {
-      const int id = tid + kPoolThreads * i;  // 0 .. 16 D - 1
-      const int d = id >> 4;                  // dim row of the tile
-      const int chunk = id & 15;              // slots chunk * 8 .. chunk * 8 + 7
-      uint32_t w[4];
+    for (int hh = 0; hh < 2; ++hh) {
+      if (my_half == hh) {
 #pragma unroll
-      for (int m = 0; m < 8; m += 2) {
-        const int s0 = chunk * 8 + m;
-        // slot -> key: chunk16 * 16 + 4 * half + (m % 4) + 8 * (m / 4)
-        const int c16 = s0 >> 4, half = (s0 >> 3) & 1, mm = s0 & 7;
-        const int key0 = c16 * 16 + 4 * half + (mm & 3) + 8 * (mm >> 2);
-        const uint32_t lo = vrows[key0 * kVPitch + d];
-        const uint32_t hi = vrows[(key0 + 1) * kVPitch + d];
-        w[m >> 1] = lo | (hi << 16);
+        for (int i = 0; i < kRowsPer; ++i) {
+          const int row = rg * kRowsPer + i - hh * (kBlock / 2);
+          uint32_t* dst = reinterpret_cast<uint32_t*>(vrows + row * kVPitch + c * 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dst[e] = vraw[i][e];
+        }
       }
-      uint16_t* dst;
-      if (D == 128)
-        dst = tile + d * kBlock + ((chunk ^ (d & 15)) << 3);
-      else
-        dst = tile + (chunk >> 2) * (D * 32) + d * 32 + (((chunk & 3) ^ ((d >> 2) & 3)) << 3);
-      *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+      block_sync();
+#pragma unroll
+      for (int i = 0; i < 8 * D / kPoolThreads; ++i) {
+        const int id = tid + kPoolThreads * i;  // 0 .. 8 D - 1
+        const int d = id >> 3;                  // dim row of the tile
+        const int chunk = hh * 8 + (id & 7);    // slots chunk * 8 .. chunk * 8 + 7 (keys of this half)
+        uint32_t w[4];
+#pragma unroll
+        for (int m = 0; m < 8; m += 2) {
+          const int s0 = chunk * 8 + m;
+          // slot -> key: chunk16 * 16 + 4 * half + (m % 4) + 8 * (m / 4)
+          const int c16 = s0 >> 4, half = (s0 >> 3) & 1, mm = s0 & 7;
+          const int key0 = c16 * 16 + 4 * half + (mm & 3) + 8 * (mm >> 2) - hh * (kBlock / 2);
+          const uint32_t lo = vrows[key0 * kVPitch + d];
+          const uint32_t hi = vrows[(key0 + 1) * kVPitch + d];
+          w[m >> 1] = lo | (hi << 16);
+        }
+        uint16_t* dst;
+        if (D == 128)
+          dst = tile + d * kBlock + ((chunk ^ (d & 15)) << 3);
+        else
+          dst = tile + (chunk >> 2) * (D * 32) + d * 32 + (((chunk & 3) ^ ((d >> 2) & 3)) << 3);
+        *reinterpret_cast<u32x4*>(dst) = u32x4{w[0], w[1], w[2], w[3]};
+      }
+      if (hh == 0) block_sync();   // every read of the first half is done
     }
   }
   if (DO_V) {
