@@ -153,6 +153,33 @@ def test_v1_route_head_groups(gpu):
     np.testing.assert_array_equal(to_np(idx), e_idx)
 
 
+def test_v1_route_eight_chunk_rows(gpu):
+    """Rows of 257-512 key blocks take the select kernel's 8-chunk form (40000
+    tokens: 313 blocks). V1 scores against the oracle on a sample of tiles, the
+    fused mask equal to the selection rule on the kernel's own scores, and the
+    lists and counts equal to that mask's."""
+    length, q_heads, kv_heads, alpha = 40000, 8, 2, 0.3
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    q = (torch.randn(1, length, q_heads, 128, generator=gen, device="cuda") * 2).to(torch.bfloat16)
+    k = torch.randn(1, length, kv_heads, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn(1, length, kv_heads, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    backend = attention.AttentionBackend(alpha=alpha, register=False)
+    backend.configure("fp_v1", alpha)
+    record = {"events": {}}
+    _, kbar, scores, idx, cnt, sel = backend._v1_selection(q, k, SCALE, record, v, True)
+    g_scores = to_np(scores)
+    assert g_scores.shape == (1, 313, 313, q_heads)
+    tiles = [0, 1, 150, 255, 312]
+    qn, kn = to_np(q), to_np(kbar)
+    expected = ref.v1_scores(qn, kn, SCALE)
+    np.testing.assert_allclose(g_scores[:, tiles], expected[:, tiles], atol=2e-4, rtol=0.005)
+    own = ref.mask_from_indices(*ref.deal_output_score(g_scores, 2, 4, alpha, 2, 0))
+    np.testing.assert_array_equal(to_np(sel), own)
+    e_idx, e_cnt = ref.indices_from_mask(own)
+    np.testing.assert_array_equal(to_np(cnt), e_cnt)
+    np.testing.assert_array_equal(to_np(idx), e_idx)
+
+
 def _adversarial_scores(length, seed):
     """Score tensors that stress the threshold: raised-to-the-4th V1 scores
     (check_math.py:305-311), exact ties with the threshold, zero rows."""
