@@ -63,6 +63,15 @@ def test_c_abi_argument_validation_without_gpu():
                              fake, s4, None) == _lib.SPX_EUNSUPPORTED
     assert lib.spx_mean_tail(fake, s4, None, None, None, None, fake, fake, fake, 1, 256, 28, 4, 128,
                              128, ctypes.c_float(0.1), fake, s4, None, None, None) == _lib.SPX_EINVAL
+    # the routed V1 form: at most 256 q heads, an 8-byte-aligned index output (its
+    # per-block partials live there between the route's two kernels)
+    def route(heads, kv_heads, indices):
+        return lib.spx_v1_route(fake, s4, fake, s4, 1, 256, heads, kv_heads, 128, 128,
+                                ctypes.c_float(0.1), ctypes.c_float(0.08), 2, 4, 2, None, indices,
+                                fake, None, None)
+    assert route(264, 8, fake) == _lib.SPX_EUNSUPPORTED
+    assert b"q_heads" in lib.spx_last_error()
+    assert route(28, 4, ctypes.c_void_p((1 << 20) + 4)) == _lib.SPX_EINVAL
 
 
 def test_call_maps_status_to_exceptions():
