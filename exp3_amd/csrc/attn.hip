@@ -1070,9 +1070,12 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
       const int r = 4 * i + (lane >> 4), c = lane & 15;
       const u32x4 v4 = *reinterpret_cast<const u32x4*>(stage + r * kBlock + ((c ^ (r & 15)) << 3));
       const int64_t row = (int64_t)t * kBlock + wq * 32 + r;
+      // non-temporal: the output is not read again here, and its lines would only
+      // displace the K/V tiles the other items on this XCD are walking
       if (live && row < a.seq)
-        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + b * a.os_b + row * a.os_s +
-                                  h * a.os_h + c * 8) = v4;
+        __builtin_nontemporal_store(
+            v4, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + b * a.os_b + row * a.os_s +
+                                         h * a.os_h + c * 8));
     }
   }
   if (live && qrow < a.seq && a.lse && half_e == 0)

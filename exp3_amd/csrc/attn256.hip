@@ -457,9 +457,10 @@ __global__ __launch_bounds__(kA2Threads, 1) void attn256_kernel(Attn256Args a) {
       const int r = 2 * i + (lane_e >> 5), c = lane_e & 31;
       const u32x4 v4 = *reinterpret_cast<const u32x4*>(stage + r * kD2 + ((c ^ r) << 3));
       const int64_t row = (int64_t)t * kBlock + wv * 32 + r;
-      if (row < a.seq)
-        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + b * a.os_b + row * a.os_s +
-                                  h * a.os_h + c * 8) = v4;
+      if (row < a.seq)   // non-temporal: not read again here (keeps the K/V sub-blocks in L2)
+        __builtin_nontemporal_store(
+            v4, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + b * a.os_b + row * a.os_s +
+                                         h * a.os_h + c * 8));
     }
   }
   if (row_ok && a.lse && half == 0)
