@@ -589,12 +589,13 @@ __global__ __launch_bounds__(kSelectThreads) void v1_select_kernel(V1Args a) {
     if (p_off < span && hl < gh) {
       const int h = h0 + hl;
       const int n = count[h];
+      // non-temporal: the slabs are read only by later launches
       for (int p = p_off; p < NB; p += span)
-        a.indices[slab + (int64_t)p * H + h] = p < n ? (int64_t)list[hl * NB + p] : (int64_t)NB;
+        __builtin_nontemporal_store(p < n ? (int64_t)list[hl * NB + p] : (int64_t)NB, &a.indices[slab + (int64_t)p * H + h]);
       if (a.mask) {
         const uint64_t* w = words + (size_t)h * NC;
         for (int j = p_off; j < NB; j += span)
-          a.mask[slab + (int64_t)j * H + h] = (uint8_t)((w[j >> 6] >> (j & 63)) & 1ull);
+          __builtin_nontemporal_store((uint8_t)((w[j >> 6] >> (j & 63)) & 1ull), &a.mask[slab + (int64_t)j * H + h]);
       }
     }
     block_sync();   // the list buffer is free for the next group
