@@ -26,26 +26,53 @@ struct MeanQArgs {
   int seq, q_heads, blocks;
 };
 
+// One workgroup per (b, tile, q head): thread (row group rg, 16-byte chunk c) loads
+// its rows' chunk c (all loads in flight at once) and sums them in fp32; the row
+// groups of a wave are combined by lane exchanges and the four waves in a fixed
+// order through LDS.
 template <int D>
 __global__ __launch_bounds__(256) void tile_mean_kernel(MeanQArgs a) {
-  const int t = blockIdx.x;
-  const int b = blockIdx.z;
-  const int idx = blockIdx.y * 256 + threadIdx.x;
-  if (idx >= a.q_heads * (D / 2)) return;
-  const int h = idx / (D / 2), d2 = idx % (D / 2);
+  constexpr int kChunks = D / 8;              // 16-byte chunks per row
+  constexpr int kGroups = 256 / kChunks;      // row groups (16 at D = 128, 8 at D = 256)
+  constexpr int kRowsPer = kBlock / kGroups;  // rows per thread
+  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c = tid % kChunks, rg = tid / kChunks;
   const int row0 = t * kBlock;
   const int n = min(kBlock, a.seq - row0);
-  const uint16_t* src = a.q + b * a.qs_b + (int64_t)row0 * a.qs_s + h * a.qs_h + 2 * d2;
-  float s0 = 0.0f, s1 = 0.0f;
-  for (int r = 0; r < n; ++r) {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(src + (int64_t)r * a.qs_s);
-    s0 += bf16_lo(w);
-    s1 += bf16_hi(w);
+  const uint16_t* src = a.q + b * a.qs_b + (int64_t)row0 * a.qs_s + h * a.qs_h + c * 8;
+  // unconditional loads (rows past the tile's end read its last row and are dropped
+  // below): no branch separates the loads, so all of them are in flight at once
+  u32x4 raw[kRowsPer];
+#pragma unroll
+  for (int i = 0; i < kRowsPer; ++i)
+    raw[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)min(rg * kRowsPer + i, n - 1) * a.qs_s);
+  float s[8] = {};
+#pragma unroll
+  for (int i = 0; i < kRowsPer; ++i) {
+    const bool ok = rg * kRowsPer + i < n;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      s[2 * e] += ok ? bf16_lo(raw[i][e]) : 0.0f;
+      s[2 * e + 1] += ok ? bf16_hi(raw[i][e]) : 0.0f;
+    }
   }
-  const float count = (float)n;
-  float* dst = a.qmean + (((int64_t)b * a.blocks + t) * a.q_heads + h) * D + 2 * d2;
-  dst[0] = s0 / count;
-  dst[1] = s1 / count;
+  // lanes of one wave holding the same chunk differ in the lane bits above the chunk
+#pragma unroll
+  for (int m = kChunks; m < 64; m <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] += __shfl_xor(s[e], m);
+  }
+  __shared__ float part[4][D];
+  if (lane < kChunks) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[w][c * 8 + e] = s[e];
+  }
+  block_sync();
+  if (tid < D) {
+    const float sum = part[0][tid] + part[1][tid] + part[2][tid] + part[3][tid];
+    a.qmean[(((int64_t)b * a.blocks + t) * a.q_heads + h) * D + tid] = sum / (float)n;
+  }
 }
 
 struct ChoiceArgs {
@@ -171,15 +198,15 @@ extern "C" int spx_tile_mean_query(const void* q, const int64_t* q_strides, int 
               batch, seq, q_heads);
   SPX_REQUIRE(q && q_strides && qmean, SPX_EINVAL, "null pointer");
   SPX_REQUIRE(q_strides[3] == 1, SPX_EINVAL, "q: innermost (dim) stride must be 1");
-  SPX_REQUIRE((reinterpret_cast<uintptr_t>(q) & 3) == 0 && q_strides[0] % 2 == 0 &&
-                  q_strides[1] % 2 == 0 && q_strides[2] % 2 == 0,
-              SPX_EINVAL, "q: base and strides must keep dim pairs 4-byte aligned");
+  SPX_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15) == 0 && q_strides[0] % 8 == 0 &&
+                  q_strides[1] % 8 == 0 && q_strides[2] % 8 == 0,
+              SPX_EINVAL, "q: base must be 16-byte aligned and batch / sequence / head strides multiples of 8 elements");
   MeanQArgs a{};
   a.q = static_cast<const uint16_t*>(q);
   a.qs_b = q_strides[0]; a.qs_s = q_strides[1]; a.qs_h = q_strides[2];
   a.qmean = qmean;
   a.seq = seq; a.q_heads = q_heads; a.blocks = num_blocks(seq);
-  dim3 grid(a.blocks, (q_heads * (head_dim / 2) + 255) / 256, batch);
+  dim3 grid(a.blocks, q_heads, batch);
   if (head_dim == 256) tile_mean_kernel<256><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   else tile_mean_kernel<kHeadDim><<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
   return launch_status("tile_mean_query");

@@ -252,8 +252,9 @@ int spx_merge_exact_mean(const void* exact_out, const int64_t* exact_strides,
 /* ---------------------------------------------------------- rescue tail */
 
 /* Mean query of every query tile over its real rows: fp32 [B, NB, Hq, D]
- * (contiguous, caller-allocated). Replaces the q_mean of kernels.py:274-276
- * (rescue_tail). */
+ * (contiguous, caller-allocated). q: unit dim stride, 16-byte aligned base, batch /
+ * sequence / head strides multiples of 8 elements (as for the other Q inputs).
+ * Replaces the q_mean of kernels.py:274-276 (rescue_tail). */
 int spx_tile_mean_query(const void* q, const int64_t* q_strides, int batch, int seq, int q_heads,
                         int head_dim, int block_size, float* qmean, void* stream);
 
