@@ -161,9 +161,9 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return wave_reduce_dpp(v, 0.0f, [](float a, float b) { return a + b; });
 }
 
-// V1 selection (upstream :357-407 with min_budget = 0) of one normalised score row
-// held in registers by one wave (block c * 64 + lane in sv[c]): the same rule as
-// select_row, one ballot per 64 key blocks. Bit lane of words[c] says whether
+// Selection of one score row held in registers by one wave (block c * 64 + lane in
+// sv[c]): the same rule as select_row (V1, upstream :357-407 with min_budget = 0, or
+// the protected selection of kernels.py:129-151), one ballot per 64 key blocks. Bit lane of words[c] says whether
 // block c * 64 + lane is selected (c < ceil(kb / 64)); returns the count.
 constexpr int kRowChunks = kMaxBlocks / 64;
 template <int NC>
@@ -180,14 +180,16 @@ __device__ __forceinline__ int select_v1_row_bits(const float (&sv)[NC], int t,
   const float maximum = wave_max_dpp(local);
   const float threshold = maximum * p.alpha;   // fp32(max * fp32(alpha))
   const bool last_rows = t >= p.query_blocks - p.last;
+  const bool protected_mode = p.mode == kSelectProtected;
+  const bool all_causal = protected_mode && p.alpha == 0.0f;
   int count = 0;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     if (c < nch) {   // wave-uniform
       const int j = c * 64 + lane;
-      const bool keep = sv[c] >= threshold;
+      const bool keep = protected_mode ? (sv[c] > 0.0f && sv[c] >= threshold) : sv[c] >= threshold;
       const int distance = t - j;
-      const bool prot = j < p.sink || (distance >= 0 && distance < p.window) || last_rows;
+      const bool prot = all_causal || j < p.sink || (distance >= 0 && distance < p.window) || last_rows;
       const bool active = j < kb && (keep || prot) && distance >= 0;
       const uint64_t ballot = __ballot(active);
       if (lane == 0) words[c] = ballot;
@@ -526,6 +528,63 @@ __host__ __device__ constexpr size_t v1_select_lds_bytes(int heads, int nc) {
   return (size_t)heads * ((size_t)nc * 8 + 4) + (size_t)kSelectListEntries * 2;
 }
 
+// The tile's outputs once every row's selection words and count are in LDS (and
+// every input read): counts, then the [KB, H] index and mask slabs, in groups of
+// heads whose lists fit the LDS list buffer (one group unless H * KB > 32768); each
+// group's rows are compacted from their words into LDS lists, then entry (p, h) is
+// the p-th selected block of row h, or KB past the row's count. Written with
+// consecutive lanes on consecutive entries (whole cache lines), non-temporally (the
+// slabs are read only by later launches). Null outputs are skipped.
+template <int NC>
+__device__ __forceinline__ void write_tile_slabs(const uint64_t* words, const int* count,
+                                                 uint16_t* list, int H, int KB, int nch,
+                                                 int64_t slab, int64_t count_base,
+                                                 int64_t* indices, int32_t* counts,
+                                                 uint8_t* mask) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int kWaves = kSelectThreads / 64;
+  if (counts && tid < H) counts[count_base + tid] = count[tid];
+  const int group = min(H, kSelectListEntries / KB);   // >= 32 (KB <= 1024)
+  const int span = kSelectThreads / group;              // positions per sweep
+  const int p_off = tid / group, hl = tid - p_off * group;
+  for (int h0 = 0; h0 < H; h0 += group) {
+    const int gh = min(group, H - h0);
+    if (indices) {
+      // lists of the group's rows, compacted from their words
+      for (int r = wave; r < gh; r += kWaves) {
+        const uint64_t* w = words + (size_t)(h0 + r) * NC;
+        int base = 0;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          if (c < nch) {
+            const uint64_t m = w[c];
+            if ((m >> lane) & 1ull)
+              list[r * KB + base + __popcll(m & ((1ull << lane) - 1ull))] = (uint16_t)(c * 64 + lane);
+            base += __popcll(m);
+          }
+        }
+      }
+    }
+    block_sync();
+    if (p_off < span && hl < gh) {
+      const int h = h0 + hl;
+      if (indices) {
+        const int n = count[h];
+        for (int p = p_off; p < KB; p += span)
+          __builtin_nontemporal_store(p < n ? (int64_t)list[hl * KB + p] : (int64_t)KB,
+                                      &indices[slab + (int64_t)p * H + h]);
+      }
+      if (mask) {
+        const uint64_t* w = words + (size_t)h * NC;
+        for (int j = p_off; j < KB; j += span)
+          __builtin_nontemporal_store((uint8_t)((w[j >> 6] >> (j & 63)) & 1ull),
+                                      &mask[slab + (int64_t)j * H + h]);
+      }
+    }
+    block_sync();   // the list buffer is free for the next group
+  }
+}
+
 template <int NC>   // NC >= ceil(NB / 64) chunks of 64 key blocks per row
 __global__ __launch_bounds__(kSelectThreads) void v1_select_kernel(V1Args a) {
   extern __shared__ __align__(8) unsigned char sel_lds[];
@@ -565,41 +624,8 @@ __global__ __launch_bounds__(kSelectThreads) void v1_select_kernel(V1Args a) {
     if (lane == 0) count[h] = n;
   }
   block_sync();   // every partial of the slab has been read
-  if (tid < H) a.counts[((int64_t)b * NB + t) * H + tid] = count[tid];
-  const int group = min(H, kSelectListEntries / NB);   // >= 32 (NB <= 1024)
-  const int span = kSelectThreads / group;              // positions per sweep
-  const int p_off = tid / group, hl = tid - p_off * group;
-  for (int h0 = 0; h0 < H; h0 += group) {
-    const int gh = min(group, H - h0);
-    // lists of the group's rows, compacted from their words
-    for (int r = wave; r < gh; r += kWaves) {
-      const uint64_t* w = words + (size_t)(h0 + r) * NC;
-      int base = 0;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        if (c < nch) {
-          const uint64_t m = w[c];
-          if ((m >> lane) & 1ull)
-            list[r * NB + base + __popcll(m & ((1ull << lane) - 1ull))] = (uint16_t)(c * 64 + lane);
-          base += __popcll(m);
-        }
-      }
-    }
-    block_sync();
-    if (p_off < span && hl < gh) {
-      const int h = h0 + hl;
-      const int n = count[h];
-      // non-temporal: the slabs are read only by later launches
-      for (int p = p_off; p < NB; p += span)
-        __builtin_nontemporal_store(p < n ? (int64_t)list[hl * NB + p] : (int64_t)NB, &a.indices[slab + (int64_t)p * H + h]);
-      if (a.mask) {
-        const uint64_t* w = words + (size_t)h * NC;
-        for (int j = p_off; j < NB; j += span)
-          __builtin_nontemporal_store((uint8_t)((w[j >> 6] >> (j & 63)) & 1ull), &a.mask[slab + (int64_t)j * H + h]);
-      }
-    }
-    block_sync();   // the list buffer is free for the next group
-  }
+  write_tile_slabs<NC>(words, count, list, H, NB, nch, slab, ((int64_t)b * NB + t) * H, a.indices,
+                       a.counts, a.mask);
 }
 
 // ------------------------------------------------------- score selection
@@ -633,6 +659,39 @@ __global__ __launch_bounds__(kRouteThreads) void select_kernel(SelectArgs a) {
   o.row_base = (((int64_t)b * a.sel.query_blocks + t) * kb) * a.heads + h;
   o.count_off = ((int64_t)b * a.sel.query_blocks + t) * a.heads + h;
   select_row(row, t, a.sel, o, scratch, wave_counts);
+}
+
+// Selection of every score row of a (b, t) at once, the same rule as select_kernel
+// when min_budget is 0: one workgroup per (b, t), wave w taking heads w, w + 16, ...;
+// each row is read into registers (its key blocks ss_j apart; the tile's heads share
+// the cache lines), reduced to ballot words in LDS, and the tile's counts, index and
+// mask slabs are written by write_tile_slabs.
+template <int NC>   // NC >= ceil(KB / 64)
+__global__ __launch_bounds__(kSelectThreads) void select_rows_kernel(SelectArgs a) {
+  extern __shared__ __align__(8) unsigned char sel_lds[];
+  const int H = a.heads, KB = a.sel.key_blocks, QB = a.sel.query_blocks;
+  uint64_t* words = reinterpret_cast<uint64_t*>(sel_lds);          // [H][NC]
+  int* count = reinterpret_cast<int*>(words + (size_t)H * NC);     // [H]
+  uint16_t* list = reinterpret_cast<uint16_t*>(count + H);         // [group heads][KB]
+  const int b = (int)blockIdx.x % a.batch;
+  const int t = QB - 1 - (int)blockIdx.x / a.batch;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nch = (KB + 63) >> 6;
+  const float* row0 = a.score + b * a.ss_b + t * a.ss_t;
+  for (int h = wave; h < H; h += kSelectThreads / 64) {
+    float sv[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      sv[c] = 0.0f;
+      // lanes past the row read its last entry; the rule ignores entries j >= KB
+      if (c < nch) sv[c] = row0[min(c * 64 + lane, KB - 1) * a.ss_j + h * a.ss_h];
+    }
+    const int n = select_v1_row_bits(sv, t, a.sel, words + (size_t)h * NC);
+    if (lane == 0) count[h] = n;
+  }
+  block_sync();
+  write_tile_slabs<NC>(words, count, list, H, KB, nch, (((int64_t)b * QB + t) * KB) * H,
+                       ((int64_t)b * QB + t) * H, a.indices, a.counts, a.mask);
 }
 
 // Mask -> sorted indices (kernels.py:154-160) reuses select_row in "all causal"
@@ -847,8 +906,20 @@ static int launch_select(int mode, const float* score, const int64_t* score_stri
   a.indices = indices;
   a.counts = counts;
   a.mask = mask;
-  const int grid = batch * query_blocks * heads;
-  select_kernel<<<grid, kRouteThreads, 0, static_cast<hipStream_t>(stream)>>>(a);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (min_budget == 0 && heads <= kSelectMaxHeads) {
+    const int nch = (key_blocks + 63) / 64;
+    const int grid = batch * query_blocks;
+    constexpr int T = kSelectThreads;
+    if (nch <= 1) select_rows_kernel<1><<<grid, T, v1_select_lds_bytes(heads, 1), st>>>(a);
+    else if (nch <= 2) select_rows_kernel<2><<<grid, T, v1_select_lds_bytes(heads, 2), st>>>(a);
+    else if (nch <= 4) select_rows_kernel<4><<<grid, T, v1_select_lds_bytes(heads, 4), st>>>(a);
+    else if (nch <= 8) select_rows_kernel<8><<<grid, T, v1_select_lds_bytes(heads, 8), st>>>(a);
+    else select_rows_kernel<16><<<grid, T, v1_select_lds_bytes(heads, 16), st>>>(a);
+  } else {
+    // the min_budget rank (or more than 256 heads): one workgroup per row
+    select_kernel<<<batch * query_blocks * heads, kRouteThreads, 0, st>>>(a);
+  }
   return launch_status("select");
 }
 

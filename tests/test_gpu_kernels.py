@@ -231,6 +231,26 @@ def test_protected_selection_bit_exact(gpu, length):
         np.testing.assert_array_equal(to_np(back), expected)
 
 
+def test_selection_eight_chunk_rows_bit_exact(gpu):
+    """Score rows of 257-512 key blocks (313 here, batch 2) take the per-tile
+    selection kernel's 8-chunk form: the protected selection (alpha 0 and 0.3) and
+    the V1 threshold lists equal the oracle's bit for bit, with zero rows and exact
+    threshold ties planted."""
+    rng = np.random.default_rng(37)
+    scores = rng.random((2, 313, 313, 8), dtype=np.float32) ** 4
+    scores[:, 5] = 0.0                                     # a zero row
+    scores[:, :, 3, :] = 1.0                               # the max
+    scores[:, :, 4, :] = np.float32(np.float32(1.0) * np.float32(0.3))   # exactly at 0.3 x max
+    sg = torch.from_numpy(scores).cuda()
+    for alpha in (0.0, 0.3):
+        mask = kernels.protected_selection(sg, alpha, 2, 4, 2)
+        np.testing.assert_array_equal(to_np(mask), ref.protected_selection(scores, alpha, 2, 4, 2))
+    idx, cnt = up.deal_output_score(sg, 2, 4, 0.3, 2, 0)
+    e_idx, e_cnt = ref.deal_output_score(scores, 2, 4, 0.3, 2, 0)
+    np.testing.assert_array_equal(to_np(idx), e_idx)
+    np.testing.assert_array_equal(to_np(cnt), e_cnt)
+
+
 @pytest.mark.parametrize("length", (257, 1089, 4500))   # 4500: 36 blocks, two 32-block chunks
 @pytest.mark.parametrize("selector", ("mean_balanced", "cgf_mean", "dispersion_mean"))
 def test_selector_scores(gpu, length, selector):
