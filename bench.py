@@ -20,13 +20,15 @@ Also reported on the same line:
                 the headline table plus fp_v1_rescue and fp_v1_rescue_v2);
   stages        per-stage kernel times with their roofline fractions;
   full_model    the metric's second half: random-init Qwen2.5-7B (28 layers) prefill of
-                32640 ids, median of rotated repeats as evaluate.py times it, for dense
-                (torch SDPA under the reference's backend pin), fp_v1, mean_native and
-                dense through the HIP kernel;
+                32640 ids, median of rotated repeats as evaluate.py times it, with peak
+                allocated / reserved memory, for every method (dense through torch SDPA
+                under the reference's backend pin) and dense through the HIP kernel;
   cpu_baseline  the CPU oracle (numpy restatement of the reference path) on a
-                bounded sample of the same workload, scaled to ms per layer; plus
-                BASELINE config 1 (S=4096) through the oracle in full beside the same
-                layer on the GPU (--cpu-all-methods: the 32K sample for every method).
+                bounded sample of the same workload, scaled to ms per layer, with the
+                GPU routing's threshold ties against the oracle's; the same for every
+                method (per_method); BASELINE config 1 (S=4096) through the oracle in
+                full beside the same layer on the GPU; BASELINE config 5 (S=131072,
+                cgf_mean) on sampled query tiles beside the GPU layer.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -65,8 +67,13 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample-tiles", type=int, default=4, help="minimum sampled query tiles")
     p.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of sampled attention")
-    p.add_argument("--cpu-all-methods", action="store_true",
-                   help="also time the CPU oracle for every method (several minutes)")
+    p.add_argument("--cpu-headline-only", action="store_true",
+                   help="time the CPU oracle for the headline method only (not every method "
+                        "and not config 5)")
+    p.add_argument("--cpu-method-budget", type=float, default=8.0,
+                   help="seconds of sampled attention per method in the per-method CPU baseline")
+    p.add_argument("--cpu-config5-budget", type=float, default=15.0,
+                   help="seconds of sampled tiles in the config-5 CPU baseline")
     p.add_argument("--traffic-file", default=str(ROOT / "profiles" / "hbm_traffic.json"))
     p.add_argument("--no-full-model", action="store_true",
                    help="skip the full-model 32K prefill (second half of the metric)")
@@ -76,6 +83,11 @@ def parse_args():
 
 class Layer:
     layer_idx = 0
+
+
+def progress(message):
+    """One progress line on stderr (the JSON result line goes to stdout)."""
+    print(f"bench: {message}", file=sys.stderr, flush=True)
 
 
 def timed_forward(backend, q, k, v, scale, steps, warmup, torch):
@@ -173,11 +185,11 @@ def _cpu_model():
 
 def _oracle_route(ref, qn, kn, vn, scale, method, alpha):
     """The oracle's routing for ``method`` (attention_layer's first half):
-    (indices, counts, selected, descriptors, rescue choice)."""
+    (indices, counts, selected, descriptors, rescue choice, routing scores)."""
     import numpy as np
     batch, seq, heads, _ = qn.shape
     blocks = ref.num_blocks(seq)
-    desc = None
+    desc = scores = None
     if method == "dense":
         sel = np.broadcast_to(np.arange(blocks)[None, :, None, None]
                               >= np.arange(blocks)[None, None, :, None], (batch, blocks, blocks, heads))
@@ -195,14 +207,14 @@ def _oracle_route(ref, qn, kn, vn, scale, method, alpha):
         sel = ref.protected_selection(scores, alpha, 2, 4, 2)
         idx, cnt = ref.indices_from_mask(sel)
     choice = ref.rescue_choice(qn, kn, precision="f32") if method in ref.RESCUE_METHODS else None
-    return idx, cnt, sel, desc, choice
+    return idx, cnt, sel, desc, choice, scores
 
 
 def _oracle_tiles(ref, qn, kn, vn, scale, method, route, tiles):
     """The oracle's attention part of the layer for the given query tiles (all
     tiles for None); rows outside the tiles are left as the exact part's zeros."""
     import numpy as np
-    idx, cnt, sel, desc, choice = route
+    idx, cnt, sel, desc, choice = route[:5]
     out, lse = ref.exact_attention(qn, kn, vn, idx, cnt, scale, precision="f32", tiles=tiles)
     if method in ref.MEAN_METHODS:
         t_out, t_lse = ref.mean_tail(qn, desc, sel, scale, precision="f32", tiles=tiles)
@@ -223,9 +235,10 @@ def full_model_prefill(seq, alpha, seed, repeats, probe, torch):
     random-init Qwen2.5-7B (28 layers, bf16) prefilling ``seq`` seeded token ids with
     the backend registered as transformers' "sdpa" attention, timed as the
     reference's evaluate.py:323-345 / 630-663 (warm-up per case, ``repeats``
-    rotated rounds, median) inside the SDPA backend pin of evaluate.py:630.
-    Cases: dense through torch SDPA (the reference's dense), fp_v1 and mean_native
-    at ``alpha``, and dense through the HIP attention kernel (like for like)."""
+    rotated rounds, median, peak allocated / reserved memory per prefill) inside
+    the SDPA backend pin of evaluate.py:630. Cases: every method at ``alpha``
+    (dense through torch SDPA, the reference's dense) and dense through the HIP
+    attention kernel (like for like)."""
     from exp3_amd import attention
     from measure import sweeps
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
@@ -237,12 +250,20 @@ def full_model_prefill(seq, alpha, seed, repeats, probe, torch):
         model = sweeps.build_qwen2_7b(28, seed)
         build_s = time.perf_counter() - t0
         ids = sweeps.prompt_ids(seq, seed, model.config.vocab_size)
-        cases = [("dense", "dense", "sdpa"), ("fp_v1", "fp_v1", "sdpa"),
-                 ("mean_native", "mean_native", "sdpa"), ("dense_hip", "dense", "hip")]
-        times, tokens = sweeps.time_prefills(model, backend, ids, cases, repeats, alpha, context)
+        cases = [(m, m, "sdpa") for m in attention.METHODS] + [("dense_hip", "dense", "hip")]
+        times, tokens, peaks = sweeps.time_prefills(model, backend, ids, cases, repeats, alpha,
+                                                    context)
     finally:
         ALL_ATTENTION_FUNCTIONS["sdpa"] = saved
     med = {label: sweeps.median(v) for label, v in times.items()}
+    per_method = {
+        label: {"prefill_ms": round(med[label], 1),
+                "speedup_vs_dense": round(med["dense"] / med[label], 3),
+                "peak_allocated_gib": round(max(p[0] for p in peaks[label]), 3),
+                "peak_reserved_gib": round(max(p[1] for p in peaks[label]), 3),
+                "all_ms": [round(x, 1) for x in times[label]],
+                "first_token_id": tokens[label]}
+        for label in times}
     result = {
         "seq": seq, "layers": 28, "model": "random-init Qwen2.5-7B architecture, bf16",
         "alpha": alpha, "repeats": repeats, "median_of": "rotated repeats (evaluate.py:646-663)",
@@ -253,8 +274,7 @@ def full_model_prefill(seq, alpha, seed, repeats, probe, torch):
         "dense_hip_ms": round(med["dense_hip"], 1),
         "speedup": round(med["dense"] / med["mean_native"], 3),
         "speedup_vs_dense_hip": round(med["dense_hip"] / med["mean_native"], 3),
-        "all_ms": {label: [round(x, 1) for x in v] for label, v in times.items()},
-        "first_token_ids": tokens,
+        "methods": per_method,
         "model_build_s": round(build_s, 1),
     }
     del model
@@ -262,10 +282,59 @@ def full_model_prefill(seq, alpha, seed, repeats, probe, torch):
     return result
 
 
-def cpu_baseline(q, k, v, scale, method, alpha, sample_tiles, budget_s):
+def routing_ties(gpu_scores, gpu_sel, scores, sel, alpha, positive_rule, eps=1e-6, tiles=None):
+    """Threshold ties of one routing against the oracle's: routed entries (causal,
+    outside the sink / window / last query blocks) whose oracle score lies within
+    ``eps`` of its row's threshold fp32(max * alpha) (or of 0 under the selectors'
+    positive-score rule), how many of those the GPU mask sets differently, and how
+    many entries differ anywhere else (0 when the masks agree up to ties)."""
+    import numpy as np
+    shape = sel.shape
+    t = np.arange(shape[1]).reshape(1, -1, 1, 1)
+    j = np.arange(shape[2]).reshape(1, 1, -1, 1)
+    routed = (j <= t - 4) & (j >= 2) & (t < shape[1] - 2)
+    if tiles is not None:
+        routed = routed & np.isin(np.arange(shape[1]), tiles).reshape(1, -1, 1, 1)
+    routed = np.broadcast_to(routed, shape)
+    thr = (scores.max(axis=2, keepdims=True).astype(np.float32) * np.float32(alpha))
+    near = np.abs(scores.astype(np.float64) - thr.astype(np.float64)) <= eps
+    if positive_rule:
+        near |= np.abs(scores) <= eps
+    rows = slice(None) if tiles is None else tiles
+    differ = np.zeros(shape, bool)
+    differ[:, rows] = gpu_sel[:, rows] != sel[:, rows]
+    ties = near & routed
+    return {"routed_entries": int(np.count_nonzero(routed)),
+            "tie_entries": int(np.count_nonzero(ties)),
+            "differ_at_ties": int(np.count_nonzero(differ & near)),
+            "differ_elsewhere": int(np.count_nonzero(differ & ~near)),
+            "max_abs_score_diff": float(np.abs(gpu_scores[:, rows].astype(np.float64)
+                                               - scores[:, rows]).max()),
+            "eps": eps}
+
+
+def gpu_routing(qg, kg, vg, scale, method, alpha):
+    """The GPU's routing scores and selection mask (numpy) for ``method``, from the
+    kernels ``forward`` launches."""
+    from exp3_amd import attention, kernels
+    backend = attention.AttentionBackend(alpha=alpha, register=False)
+    backend.configure(method, alpha)
+    record = {"events": {}}
+    if method in attention.V1_ROUTED_METHODS:
+        values = vg if method in ("mean_native", "fp_v1_rescue_v2") else None
+        _, _, scores, _, _, sel = backend._v1_selection(qg, kg, scale, record, values, True)
+    else:
+        desc, _, _, _, sel = backend._new_selection(qg, kg, vg, scale, record)
+        scores = kernels.selector_scores(qg, desc, scale, method)
+    return scores.float().cpu().numpy(), sel.cpu().numpy()
+
+
+def cpu_baseline(q, k, v, scale, method, alpha, sample_tiles, budget_s, gpu=None):
     """Time the CPU oracle (reference semantics in numpy float32) on the full
     routing stages plus a sample of query tiles of the attention stages; scale
-    the sampled part by selected-block work to a whole layer."""
+    the sampled part by selected-block work to a whole layer. With ``gpu`` (the
+    same inputs on the device) the GPU routing is compared with the oracle's and
+    its threshold ties are recorded."""
     import numpy as np
     from oracle import reference_cpu as ref
     qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
@@ -273,6 +342,11 @@ def cpu_baseline(q, k, v, scale, method, alpha, sample_tiles, budget_s):
     t0 = time.perf_counter()
     route = _oracle_route(ref, qn, kn, vn, scale, method, alpha)
     routing_s = time.perf_counter() - t0
+    ties = None
+    if gpu is not None and route[5] is not None:
+        g_scores, g_sel = gpu_routing(*gpu, scale, method, alpha)
+        ties = routing_ties(g_scores, g_sel, route[5], route[2], alpha,
+                            positive_rule=method not in ref.V1_ROUTED)
     # query tiles in a stratified order (coarse to fine over the sequence) until the
     # time budget is spent, so the sample is spread over short and long tiles
     order = []
@@ -293,7 +367,7 @@ def cpu_baseline(q, k, v, scale, method, alpha, sample_tiles, budget_s):
     work = route[1].sum(axis=(0, 2)).astype(np.float64) + 1.0   # per tile (+1: the tail row pass)
     scale_up = work.sum() / work[tiles].sum()
     total_ms = (routing_s + attention_s * scale_up) * 1000.0
-    return {
+    result = {
         "value": round(total_ms, 1),
         "unit": "ms",
         "cores": int(_cpu_threads()),
@@ -303,8 +377,92 @@ def cpu_baseline(q, k, v, scale, method, alpha, sample_tiles, budget_s):
                    f"query tiles spread over the sequence ({attention_s:.1f} s) scaled x{scale_up:.1f} "
                    f"by selected-block work; numpy float32 oracle (reference's own harness pins "
                    f"1 thread, evaluate.py:793)"),
+        "routing_s": round(routing_s, 2),
+        "attention_sample_s": round(attention_s, 2),
+        "sampled_tiles": len(tiles),
         "cpu": _cpu_model(),
     }
+    if ties is not None:
+        result["ties"] = ties
+    return result
+
+
+def cpu_config5(seed, alpha, budget_s, torch, method="cgf_mean", seq=131072, needles=256):
+    """BASELINE config 5 on the CPU: S=131072 with 256 planted needles, ``method`` at
+    ``alpha``. The oracle runs the descriptors over the whole sequence, then scores,
+    selects and attends (exact blocks + mean tail + merge) sampled query tiles, one
+    at a time in the order 255, 511, 767, 1023, 127, 383, ... until ``budget_s``: a
+    tile's selector scores depend on its own rows only, and its attention on the
+    sequence up to its last row, so each tile runs on the prefix that ends with it.
+    The layer estimate scales the sampled per-tile time by causal work (t + 1 blocks
+    per tile; selection density is 1.0 on these inputs). The same layer runs on the
+    GPU beside it; the sampled tiles' GPU scores, masks and outputs are compared
+    with the oracle's."""
+    import numpy as np
+    from oracle import reference_cpu as ref
+    from exp3_amd import attention, synthetic
+    q, k, v, _ = synthetic.make_inputs(seq, seed=seed, needles=needles)
+    scale = 128 ** -0.5
+    qn, kn, vn = (x.float().numpy() for x in (q, k, v))
+    qg, kg, vg = q.cuda(), k.cuda(), v.cuda()
+    backend = attention.AttentionBackend(alpha=alpha, register=False)
+    backend.configure(method, alpha)
+    gpu_ms = timed_forward(backend, qg, kg, vg, scale, 3, 1, torch)
+    out, _ = backend.forward(Layer(), qg.transpose(1, 2), kg.transpose(1, 2), vg.transpose(1, 2),
+                             None, scale)
+    out = out.float().cpu().numpy()
+    g_scores, g_sel = gpu_routing(qg, kg, vg, scale, method, alpha)
+    del qg, kg, vg
+    torch.cuda.empty_cache()
+    blocks = ref.num_blocks(seq)
+    order, step = [], 256
+    while step >= 1 and len(order) < blocks:
+        for t in range(step - 1, blocks, step):
+            if t not in order:
+                order.append(t)
+        step //= 2
+    t0 = time.perf_counter()
+    desc = ref.block_descriptors(kn, vn, precision="f32")
+    desc_s = time.perf_counter() - t0
+    scores = np.zeros((1, blocks, blocks, qn.shape[2]), np.float32)
+    tiles, tile_s, max_abs, mean_abs = [], 0.0, 0.0, []
+    for t in order:
+        end = min(seq, (t + 1) * 128)
+        prefix = ref.BlockDescriptors(desc.mean_k[:, :t + 1], desc.mean_v[:, :t + 1],
+                                      desc.var_k[:, :t + 1], desc.sigma_v[:, :t + 1],
+                                      desc.counts[:t + 1])
+        t1 = time.perf_counter()
+        row = ref.selector_scores(qn[:, :end], prefix, scale, method, precision="f32",
+                                  tiles=[t])[:, t]
+        scores[:, t, :t + 1] = row
+        sel = ref.protected_selection(scores, alpha, 2, 4, 2)   # row t's rule needs NB
+        expected, _ = ref.attention_from_selection(qn[:, :end], kn[:, :end], vn[:, :end], scale,
+                                                   method, sel[:, :t + 1, :t + 1], prefix,
+                                                   precision="f32", tiles=[t])
+        tile_s += time.perf_counter() - t1
+        tiles.append(t)
+        if (g_sel[:, t] == sel[:, t]).all():
+            diff = np.abs(out[:, t * 128:end] - expected[:, t * 128:end])
+            max_abs = max(max_abs, float(diff.max()))
+            mean_abs.append(float(diff.mean()))
+        if len(tiles) >= 2 and tile_s >= budget_s:
+            break
+    sel = ref.protected_selection(scores, alpha, 2, 4, 2)
+    ties = routing_ties(g_scores, g_sel, scores, sel, alpha, positive_rule=True, tiles=tiles)
+    work = np.arange(1, blocks + 1, dtype=np.float64)
+    scale_up = work.sum() / work[tiles].sum()
+    cpu_ms = (desc_s + tile_s * scale_up) * 1000.0
+    return {"config": "BASELINE config 5", "method": method, "alpha": alpha, "seq": seq,
+            "needles": needles, "cpu_ms": round(cpu_ms, 1), "cpu_cores": int(_cpu_threads()),
+            "kind": "port",
+            "sample": (f"descriptors over all {seq} tokens ({desc_s:.1f} s); selector scores, "
+                       f"protected selection and attention (exact + mean tail + merge) of "
+                       f"{len(tiles)} query tiles {tiles}, each on its prefix ({tile_s:.1f} s), "
+                       f"scaled x{scale_up:.1f} by causal work (t + 1 blocks per tile)"),
+            "gpu_ms": round(gpu_ms, 3), "ties": ties,
+            "max_abs_gpu_vs_cpu": max_abs,
+            "mean_abs_gpu_vs_cpu": float(np.mean(mean_abs)) if mean_abs else None,
+            "compared_tiles": len(mean_abs)}
 
 
 def cpu_config1(method, alpha, seed, torch):
@@ -415,25 +573,40 @@ def main():
         methods["dense_hip"] = {"ms_per_layer": round(timed_forward(b, qg, kg, vg, scale, 5, 2, torch), 3),
                                 "block_density": 1.0}
 
+    progress("layer, stages and methods timed")
     achievable = achievable_peaks(torch)
     sdpa_context.__exit__(None, None, None)
 
     full_model = None
     if not args.no_full_model:
+        progress("full-model prefills")
         full_model = full_model_prefill(args.seq, args.alpha, args.seed, args.model_repeats,
                                         sdpa_probe, torch)
         full_model["sdpa_probe"] = sdpa_probe
 
     baseline = None
     if not args.no_cpu_baseline:
+        progress("CPU baseline")
         baseline = cpu_baseline(q, k, v, scale, args.method, args.alpha, args.cpu_sample_tiles,
-                                args.cpu_budget)
+                                args.cpu_budget, gpu=(qg, kg, vg))
         baseline["config1"] = cpu_config1(args.method, args.alpha, args.seed, torch)
-        if args.cpu_all_methods:
-            baseline["per_method"] = {
-                name: cpu_baseline(q, k, v, scale, name, args.alpha, args.cpu_sample_tiles,
-                                   args.cpu_budget)
-                for name in attention.METHODS}
+        if not args.cpu_headline_only:
+            per_method = {}
+            for name in attention.METHODS:
+                if name == args.method:
+                    entry = {key: val for key, val in baseline.items() if key != "config1"}
+                else:
+                    entry = cpu_baseline(q, k, v, scale, name, args.alpha, 2,
+                                         args.cpu_method_budget, gpu=(qg, kg, vg))
+                if name in methods:
+                    entry["gpu_ms"] = methods[name]["ms_per_layer"]
+                per_method[name] = entry
+                progress(f"CPU baseline {name}: {entry['value']} ms")
+            baseline["per_method"] = per_method
+            del qg, kg, vg
+            torch.cuda.empty_cache()
+            progress("CPU baseline config 5")
+            baseline["config5"] = cpu_config5(args.seed, 0.04, args.cpu_config5_budget, torch)
 
     line = {
         "metric": "sparse-prefill attn ms/layer @32K Qwen2.5-7B shape; full-model prefill ms",

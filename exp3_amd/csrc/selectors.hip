@@ -46,6 +46,7 @@ struct SplitArgs {
   uint16_t* ws;         // [B, Hkv, NC, D / 128, 4, 32, 128] bf16
   int batch, kv_heads, blocks, chunks, dim;
   bool second_order;
+  float mu_mul, var_mul;  // fp32 factors applied before the split (1 keeps the values)
 };
 
 __device__ __forceinline__ void split8(const float* v, u32x4& hi, u32x4& lo) {
@@ -75,12 +76,12 @@ __global__ __launch_bounds__(256) void selector_split_kernel(SplitArgs a) {
     const f32x4 m0 = *reinterpret_cast<const f32x4*>(a.mean_k + off);
     const f32x4 m1 = *reinterpret_cast<const f32x4*>(a.mean_k + off + 4);
 #pragma unroll
-    for (int x = 0; x < 4; ++x) { mu[x] = m0[x]; mu[4 + x] = m1[x]; }
+    for (int x = 0; x < 4; ++x) { mu[x] = m0[x] * a.mu_mul; mu[4 + x] = m1[x] * a.mu_mul; }
     if (a.second_order) {
       const f32x4 v0 = *reinterpret_cast<const f32x4*>(a.var_k + off);
       const f32x4 v1 = *reinterpret_cast<const f32x4*>(a.var_k + off + 4);
 #pragma unroll
-      for (int x = 0; x < 4; ++x) { var[x] = v0[x]; var[4 + x] = v1[x]; }
+      for (int x = 0; x < 4; ++x) { var[x] = v0[x] * a.var_mul; var[4 + x] = v1[x] * a.var_mul; }
     }
   }
   const int halves = a.dim / 128, hf = c >> 4, c16 = c & 15;
@@ -432,6 +433,8 @@ int run_selectors(const void* q, const int64_t* q_strides, const float* mean_k,
   sa.batch = batch; sa.kv_heads = kv_heads; sa.blocks = blocks; sa.chunks = chunks;
   sa.dim = head_dim;
   sa.second_order = selector != SPX_SELECTOR_MEAN_BALANCED;
+  sa.mu_mul = 1.0f;
+  sa.var_mul = 1.0f;
   const int64_t threads = (int64_t)batch * kv_heads * chunks * kSelChunk * (head_dim / 8);
   selector_split_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(sa);
   int rc = launch_status("selector_split");

@@ -489,33 +489,40 @@ def time_prefills(model, backend, ids, cases, repeats, alpha, context):
     rounds in rotated case order, each prefill timed from a synchronised start
     through ``model(ids, use_cache=True, logits_to_keep=1)`` and the argmax to a
     synchronised end, all inside ``context`` (the SDPA backend pin) and inference
-    mode. ``cases``: (label, method, dense_impl). Returns label -> list of ms and
-    label -> first greedy id."""
+    mode, with the peak allocated / reserved device memory of each timed prefill
+    (torch's counters reset at its start, evaluate.py:328, 338-339). ``cases``:
+    (label, method, dense_impl). Returns label -> list of ms, label -> first greedy
+    id and label -> list of (peak allocated GiB, peak reserved GiB)."""
     import torch
 
     def prefill(method, dense_impl):
         backend.configure(method, alpha)
         backend.dense_impl = dense_impl
         torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
         t0 = time.perf_counter()
         out = model(input_ids=ids, use_cache=True, logits_to_keep=1)
         token = out.logits[:, -1].argmax(dim=-1)
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1000.0
+        peak = (torch.cuda.max_memory_allocated() / 2 ** 30,
+                torch.cuda.max_memory_reserved() / 2 ** 30)
         del out
-        return ms, int(token.item())
+        return ms, int(token.item()), peak
 
     times = {label: [] for label, _, _ in cases}
+    peaks = {label: [] for label, _, _ in cases}
     tokens = {}
     with torch.inference_mode(), context:
         for label, method, impl in cases:           # warm-up (evaluate.py:634-644)
-            _, tokens[label] = prefill(method, impl)
+            _, tokens[label], _ = prefill(method, impl)
         for r in range(repeats):                     # rotated order (evaluate.py:646-663)
             order = cases[r % len(cases):] + cases[:r % len(cases)]
             for label, method, impl in order:
-                ms, _ = prefill(method, impl)
+                ms, _, peak = prefill(method, impl)
                 times[label].append(ms)
-    return times, tokens
+                peaks[label].append(peak)
+    return times, tokens, peaks
 
 
 def median(values):
@@ -538,7 +545,7 @@ def run_model(seq, layers, repeats, seed, methods, alpha, decode_tokens, split_l
     cases = [(m, m, "sdpa") for m in methods]
     if "dense" in methods:
         cases.append(("dense_hip", "dense", "hip"))
-    times, tokens = time_prefills(model, backend, ids, cases, repeats, alpha, context)
+    times, tokens, peaks = time_prefills(model, backend, ids, cases, repeats, alpha, context)
     dense_ms = median(times["dense"]) if "dense" in times else None
     for label, method, impl in cases:
         med = median(times[label])
@@ -550,6 +557,8 @@ def run_model(seq, layers, repeats, seed, methods, alpha, decode_tokens, split_l
                           "prefill_ms_median": round(med, 1),
                           "prefill_ms_all": [round(x, 1) for x in times[label]],
                           "first_token_id": tokens[label],
+                          "peak_allocated_gib": round(max(p[0] for p in peaks[label]), 3),
+                          "peak_reserved_gib": round(max(p[1] for p in peaks[label]), 3),
                           "speedup_vs_dense": round(dense_ms / med, 3) if dense_ms else None}),
               flush=True)
     backend.dense_impl = "sdpa"

@@ -56,8 +56,13 @@ _NEG_INF = np.float32(-np.inf)
 def bf16_bits(x: np.ndarray) -> np.ndarray:
     """float32 -> bf16 bit pattern (uint16), round-to-nearest-even, NaN kept quiet."""
     x = np.ascontiguousarray(x, dtype=np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    u = x.view(np.uint32)
+    # uint32 sums cannot wrap for non-NaN patterns (at most 0xFF7FFFFF + 0x8000);
+    # NaN entries are overwritten below
+    rounded = (u >> 16) & np.uint32(1)
+    rounded += u
+    rounded += np.uint32(0x7FFF)
+    rounded >>= np.uint32(16)
     out = rounded.astype(np.uint16)
     nan = np.isnan(x)
     if nan.any():

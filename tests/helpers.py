@@ -2,6 +2,9 @@
 
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import torch
 
@@ -52,6 +55,33 @@ def threshold_ties(scores, alpha, positive_rule=False):
     if positive_rule:
         near |= np.abs(scores) <= TIE_EPS
     return near
+
+
+def routed_entries(shape, sink=2, window=4, last=2):
+    """Entries [b, t, j, h] whose selection the threshold decides: causal (j <= t)
+    and outside the protected sink, window and last query blocks."""
+    t = np.arange(shape[1]).reshape(1, -1, 1, 1)
+    j = np.arange(shape[2]).reshape(1, 1, -1, 1)
+    routed = (j <= t - window) & (j >= sink) & (t < shape[1] - last)
+    return np.broadcast_to(routed, shape)
+
+
+def record_ties(case, method, alpha, ties, differ, listed, tiles=None):
+    """Append one case's threshold-tie count (routed entries within TIE_EPS of the
+    threshold, or of 0 under the positive-score rule) and how many of them the GPU
+    mask sets differently to the JSON-lines file named by SPX_TIES_LOG, when that
+    variable is set."""
+    path = os.environ.get("SPX_TIES_LOG")
+    if not path:
+        return
+    routed = routed_entries(ties.shape)
+    if tiles is not None:
+        routed = routed & np.isin(np.arange(ties.shape[1]), tiles).reshape(1, -1, 1, 1)
+    with open(path, "a") as f:
+        f.write(json.dumps({"case": case, "method": method, "alpha": alpha,
+                            "routed_entries": int(np.count_nonzero(routed)),
+                            "tie_entries": int(np.count_nonzero(ties & routed)),
+                            "differ": int(differ), "listed": listed}) + "\n")
 
 
 def masks_equal_except_ties(actual, expected, ties):

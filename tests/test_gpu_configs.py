@@ -25,8 +25,8 @@ import torch
 from exp3_amd import attention, synthetic
 from oracle import reference_cpu as ref
 from tests.helpers import (SCALE, V1_METHODS, agreeing_tiles, assert_output_close,
-                           gpu_routing, masks_equal_except_ties, oracle_scores, select,
-                           threshold_ties, tile_rows, to_np)
+                           gpu_routing, masks_equal_except_ties, oracle_scores, record_ties,
+                           select, threshold_ties, tile_rows, to_np)
 
 pytestmark = pytest.mark.gpu
 
@@ -84,7 +84,7 @@ def _forward(case, method, alpha):
     return backend, out
 
 
-def _check_layer(case, method, alpha, sample=SAMPLE):
+def _check_layer(case, method, alpha, sample=SAMPLE, name="config"):
     backend, out = _forward(case, method, alpha)
     blocks = ref.num_blocks(case.sequence)
     if method == "dense":
@@ -102,6 +102,7 @@ def _check_layer(case, method, alpha, sample=SAMPLE):
         e_sel = select(e_scores, method, alpha)
         ties = threshold_ties(e_scores, alpha, positive_rule=family == "selector")
         bad, differ, listed = masks_equal_except_ties(g_sel, e_sel, ties)
+        record_ties(f"{name} S={case.sequence}", method, alpha, ties, differ, listed)
         assert bad == 0, f"{bad} mask entries differ away from the threshold"
         density = g_sel.sum() / (28 * blocks * (blocks + 1) / 2)
         print(f"{method} alpha={alpha}: density {density:.5f} (oracle "
@@ -119,7 +120,7 @@ def _check_layer(case, method, alpha, sample=SAMPLE):
 
 @pytest.mark.parametrize("method", SIX)
 def test_config2_six_methods(gpu, config2, method):
-    _check_layer(config2, method, 0.08)
+    _check_layer(config2, method, 0.08, name="config 2")
 
 
 CONFIG3 = [(m, a) for a in (0.04, 0.08, 0.16)
@@ -130,7 +131,7 @@ CONFIG3 += [("fp_v1", 0.08), ("dense", None)]
 @pytest.mark.parametrize("method,alpha", CONFIG3)
 def test_config3_needles(gpu, config3, method, alpha):
     assert len(config3.needles) == 64
-    _check_layer(config3, method, 0.08 if alpha is None else alpha)
+    _check_layer(config3, method, 0.08 if alpha is None else alpha, name="config 3 (64 needles)")
 
 
 LONG = 131072
@@ -162,6 +163,10 @@ def test_config5_long_context(gpu, config5, method):
     ties = threshold_ties(e_scores, alpha, positive_rule=True)
     bad, differ, listed = masks_equal_except_ties(g_sel[:, sample], e_sel[:, sample],
                                                   ties[:, sample])
+    sampled_ties = np.zeros_like(ties)
+    sampled_ties[:, sample] = ties[:, sample]
+    record_ties(f"config 5 (256 needles) S={LONG} tiles {sample}", method, alpha,
+                sampled_ties, differ, listed, tiles=sample)
     assert bad == 0, f"{bad} sampled mask entries differ away from the threshold"
     same = (g_sel[:, sample] == e_sel[:, sample]).all(axis=(0, 2, 3))
     tiles = [t for t, ok in zip(sample, same) if ok]

@@ -231,24 +231,43 @@ def test_protected_selection_bit_exact(gpu, length):
         np.testing.assert_array_equal(to_np(back), expected)
 
 
-def test_selection_eight_chunk_rows_bit_exact(gpu):
-    """Score rows of 257-512 key blocks (313 here, batch 2) take the per-tile
-    selection kernel's 8-chunk form: the protected selection (alpha 0 and 0.3) and
-    the V1 threshold lists equal the oracle's bit for bit, with zero rows and exact
-    threshold ties planted."""
-    rng = np.random.default_rng(37)
-    scores = rng.random((2, 313, 313, 8), dtype=np.float32) ** 4
+@pytest.mark.parametrize("batch,blocks,heads", [
+    (1, 100, 4),     # 2 chunks of 64 key blocks per row
+    (1, 200, 4),     # 4 chunks
+    (2, 313, 8),     # 8 chunks, batch 2
+    (1, 700, 4),     # 16 chunks
+    (1, 1024, 3),    # 16 chunks at the block limit
+    (1, 600, 64),    # 64 heads x 600 blocks > 32768 list entries: two head groups
+])
+def test_selection_row_kernel_forms_bit_exact(gpu, batch, blocks, heads):
+    """Score rows take the per-tile selection kernel in its 1-16-chunk forms (64 key
+    blocks per chunk) and, beyond 32768 list entries per tile, in several head
+    groups: the protected selection (alpha 0 and 0.3) and the V1 threshold lists
+    equal the oracle's bit for bit, with zero rows and exact threshold ties
+    planted."""
+    rng = np.random.default_rng(37 + blocks)
+    scores = rng.random((batch, blocks, blocks, heads), dtype=np.float32) ** 4
     scores[:, 5] = 0.0                                     # a zero row
     scores[:, :, 3, :] = 1.0                               # the max
     scores[:, :, 4, :] = np.float32(np.float32(1.0) * np.float32(0.3))   # exactly at 0.3 x max
+    scores[:, :, blocks - 2, :] = np.float32(0.3) * np.float32(1.0)      # a tie at the far end
     sg = torch.from_numpy(scores).cuda()
     for alpha in (0.0, 0.3):
-        mask = kernels.protected_selection(sg, alpha, 2, 4, 2)
-        np.testing.assert_array_equal(to_np(mask), ref.protected_selection(scores, alpha, 2, 4, 2))
+        # the backend's form: mask, indices and counts from one launch
+        indices = torch.empty(scores.shape, dtype=torch.int64, device="cuda")
+        counts = torch.empty(scores.shape[:2] + scores.shape[3:], dtype=torch.int32, device="cuda")
+        mask = kernels.protected_selection(sg, alpha, 2, 4, 2, indices, counts)
+        expected = ref.protected_selection(scores, alpha, 2, 4, 2)
+        np.testing.assert_array_equal(to_np(mask), expected)
+        e_idx, e_cnt = ref.indices_from_mask(expected)
+        np.testing.assert_array_equal(to_np(counts), e_cnt)
+        np.testing.assert_array_equal(to_np(indices), e_idx)
     idx, cnt = up.deal_output_score(sg, 2, 4, 0.3, 2, 0)
     e_idx, e_cnt = ref.deal_output_score(scores, 2, 4, 0.3, 2, 0)
-    np.testing.assert_array_equal(to_np(idx), e_idx)
     np.testing.assert_array_equal(to_np(cnt), e_cnt)
+    np.testing.assert_array_equal(to_np(idx), e_idx)
+    mask = kernels.mask_from_indices(idx, cnt)
+    np.testing.assert_array_equal(to_np(mask), ref.mask_from_indices(e_idx, e_cnt))
 
 
 @pytest.mark.parametrize("length", (257, 1089, 4500))   # 4500: 36 blocks, two 32-block chunks

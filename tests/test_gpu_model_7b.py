@@ -1,7 +1,8 @@
 """BASELINE config 4 in a test: the full 28-layer random-init Qwen2.5-7B architecture
 (hidden 3584, FFN 18944, 28 / 4 heads, RMSNorm 1e-6, RoPE theta 1e6, vocab 152064,
 QKV bias, bf16) prefilling 32640 token ids through the backend registered as
-transformers' "sdpa" attention function (attention.py:57), for dense and mean_native:
+transformers' "sdpa" attention function (attention.py:57), for dense, fp_v1,
+mean_native and cgf_mean:
 
 * the prefill (evaluate.py:323-345: ``model(ids, use_cache=True,
   logits_to_keep=1)``) gives finite logits, and evaluate.py:357-380's
@@ -9,8 +10,9 @@ transformers' "sdpa" attention function (attention.py:57), for dense and mean_na
   decode step) gives the same greedy id unless the top two logits are closer than
   the two flows' difference;
 * one layer's attention call, captured from inside the model, matches the oracle
-  on sampled query tiles (for mean_native through the oracle's own routing of that
-  layer's q / k / v).
+  on sampled query tiles (for the sparse methods through the oracle's own routing
+  of that layer's q / k / v: scores within check_math's tolerances, the mask equal
+  to the oracle's except entries within 1e-6 of the threshold).
 """
 
 import numpy as np
@@ -18,15 +20,16 @@ import pytest
 import torch
 
 from oracle import reference_cpu as ref
-from tests.helpers import (agreeing_tiles, assert_output_close, gpu_routing,
-                           masks_equal_except_ties, oracle_scores, select, threshold_ties,
-                           tile_rows, to_np)
+from tests.helpers import (V1_METHODS, agreeing_tiles, assert_output_close, gpu_routing,
+                           masks_equal_except_ties, oracle_scores, record_ties, select,
+                           threshold_ties, tile_rows, to_np)
 
 pytestmark = pytest.mark.gpu
 
 SEQ = 32640
 CAPTURED_LAYER = 20
 SAMPLE = (0, 1, 90, 180, 252, 254)
+SCORE_TOL = {"v1": dict(atol=2e-4, rtol=0.005), "selector": dict(atol=2e-5, rtol=2e-5)}
 
 
 @pytest.fixture(scope="module")
@@ -81,7 +84,7 @@ class _Capture:
         self.functions["sdpa"] = self.inner
 
 
-@pytest.mark.parametrize("method", ("dense", "mean_native"))
+@pytest.mark.parametrize("method", ("dense", "fp_v1", "mean_native", "cgf_mean"))
 def test_qwen2_7b_prefill_32640(qwen7b, method):
     model, backend, ids = qwen7b
     alpha = 0.08
@@ -116,12 +119,16 @@ def test_qwen2_7b_prefill_32640(qwen7b, method):
                                 (1, blocks, blocks, 28))
         tiles = list(SAMPLE)
     else:
+        family = "v1" if method in V1_METHODS else "selector"
         g_scores, g_sel = gpu_routing(backend, layer["q"], layer["k"], layer["v"], method, scale)
         e_scores = oracle_scores(qn, kn, vn, method, scale)
-        np.testing.assert_allclose(g_scores, e_scores, atol=2e-4, rtol=0.005)
+        np.testing.assert_allclose(g_scores, e_scores, **SCORE_TOL[family])
+        np.testing.assert_array_equal(g_sel, select(g_scores, method, alpha))
         e_sel = select(e_scores, method, alpha)
-        bad, differ, listed = masks_equal_except_ties(g_sel, e_sel,
-                                                      threshold_ties(e_scores, alpha))
+        ties = threshold_ties(e_scores, alpha, positive_rule=family == "selector")
+        bad, differ, listed = masks_equal_except_ties(g_sel, e_sel, ties)
+        record_ties(f"config 4 layer {CAPTURED_LAYER} S={SEQ}", method, alpha, ties, differ,
+                    listed)
         assert bad == 0
         print(f"layer {CAPTURED_LAYER}: density {g_sel.sum() / (28 * blocks * (blocks + 1) / 2):.4f},"
               f" {differ} tie entries differ: {listed}")
