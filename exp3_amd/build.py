@@ -45,8 +45,14 @@ HIPCC_FLAGS = [
 # route.hip: the V1 score reduction reads every MFMA result with VALU instructions;
 # in the VGPR form they read the accumulators in place instead of copying them out
 # of AGPRs first (16 copies per 32-block chunk and wave).
+# selectors.hip: the MFMAs accumulate in VGPRs so that the AGPR file is free to hold
+# the parked logits of up to 12 chunks (192 registers); the stored-chunk loop must
+# be unrolled in full (its register array indexed by constants), which a 12-chunk
+# body exceeds under the default unroll threshold (the array then went to scratch).
 EXTRA_FLAGS = {"attn256.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-               "route.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+               "route.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+               "selectors.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form",
+                                 "-mllvm", "-pragma-unroll-threshold=1000000"]}
 
 
 def _hipcc() -> str:

@@ -162,12 +162,13 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 }
 
 // Selection of one score row held in registers by one wave (block c * 64 + lane in
-// sv[c]): the same rule as select_row (V1, upstream :357-407 with min_budget = 0, or
-// the protected selection of kernels.py:129-151), one ballot per 64 key blocks. Bit lane of words[c] says whether
-// block c * 64 + lane is selected (c < ceil(kb / 64)); returns the count.
+// sv[c]): the same rule as select_row, chosen by p.mode (kSelectV1: upstream
+// :357-407 with min_budget = 0; kSelectProtected: kernels.py:129-151, s > 0 && s >= thr and
+// every causal block at alpha 0), one ballot per 64 key blocks. Bit lane of words[c]
+// says whether block c * 64 + lane is selected (c < ceil(kb / 64)); returns the count.
 constexpr int kRowChunks = kMaxBlocks / 64;
 template <int NC>
-__device__ __forceinline__ int select_v1_row_bits(const float (&sv)[NC], int t,
+__device__ __forceinline__ int select_row_bits(const float (&sv)[NC], int t,
                                                   const SelectParams& p, uint64_t* words) {
   const int lane = threadIdx.x & 63;
   const int kb = p.key_blocks;
@@ -620,7 +621,7 @@ __global__ __launch_bounds__(kSelectThreads) void v1_select_kernel(V1Args a) {
         if (c < nch && jj < NB) a.score[b * a.ss_b + t * a.ss_t + jj * a.ss_j + h * a.ss_h] = sv[c];
       }
     }
-    const int n = select_v1_row_bits(sv, t, a.sel, words + (size_t)h * NC);
+    const int n = select_row_bits(sv, t, a.sel, words + (size_t)h * NC);
     if (lane == 0) count[h] = n;
   }
   block_sync();   // every partial of the slab has been read
@@ -686,7 +687,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_rows_kernel(SelectArgs 
       // lanes past the row read its last entry; the rule ignores entries j >= KB
       if (c < nch) sv[c] = row0[min(c * 64 + lane, KB - 1) * a.ss_j + h * a.ss_h];
     }
-    const int n = select_v1_row_bits(sv, t, a.sel, words + (size_t)h * NC);
+    const int n = select_row_bits(sv, t, a.sel, words + (size_t)h * NC);
     if (lane == 0) count[h] = n;
   }
   block_sync();
