@@ -34,8 +34,13 @@
 //     global->LDS loads (chunk s + 1 lands while chunk s is computed); the next
 //     item's Q tile (into LDS, 16-byte chunk c of row r at c ^ (r & 15)) and first
 //     chunk are copied while the current item finishes.
-//   * selector_pair_kernel (head_dim 128, up to 256 blocks): eight waves, two per
-//     SIMD. Waves w and w + 4 hold the same 32 query rows and split the 128 dims;
+//   * selector_duo_kernel (mean_balanced, head_dim 128, up to 256 blocks): eight
+//     waves, two per SIMD, two adjacent tiles of one head per item (waves 0-3 tile
+//     t, waves 4-7 tile t - 1), each wave with all dims of its rows: every chunk
+//     copy serves both tiles and no partial products are exchanged.
+//   * selector_pair_kernel (cgf_mean and dispersion_mean, head_dim 128, up to 256
+//     blocks; their q*q split leaves the duo kernel too few registers): eight
+//     waves, two per SIMD. Waves w and w + 4 hold the same 32 query rows and split the 128 dims;
 //     chunk jc belongs to the wave of the K half jc & 1, which adds its partner's
 //     partial products (through one LDS slot per pair) to its own, folds the chunk
 //     into its rows' softmax state beside the next chunk's products, and keeps the
@@ -441,8 +446,9 @@ struct ChunkFold {   // for chunks with all 32 blocks visible (j < t)
 
 // Normalised contributions of one chunk, summed over the wave's 32 query rows per
 // block into part[w][block].
+template <int NBMAX>
 __device__ __forceinline__ void chunk_sums(float (&v)[16], float m, float inv_l, int jc, int w,
-                                           int lane, float (*part)[kSelMaxBlocks]) {
+                                           int lane, float (*part)[NBMAX]) {
   const int col = lane & 31;
 #pragma unroll
   for (int r = 0; r < 16; ++r) v[r] = exp2_fast(v[r] - m) * inv_l;
@@ -1085,6 +1091,247 @@ __global__ __launch_bounds__(kPairThreads, 1) void selector_pair_kernel(SelArgs 
   else pair_waves<SEL, S, 1>(args, L);
 }
 
+// ---------------------------------------------------------------------------
+// head_dim 128, rows of up to 256 blocks: two items per workgroup.
+//
+// One persistent workgroup of eight waves per CU takes items (tile pair t, t - 1;
+// batch; q head), heaviest first: waves 0-3 hold the 32-row groups of tile t,
+// waves 4-7 those of tile t - 1, each wave with all 128 dims of its rows (no
+// partial products to exchange). Both tiles read the same head's descriptor
+// chunks, so every chunk copied into LDS serves eight waves, and each SIMD runs
+// one wave of each tile: one wave's softmax and reduction issue beside the other's
+// products. At two waves per SIMD the registers hold the logits of the first S
+// chunks; a tile with more chunks forms the products of the rest a second time.
+// Products of all 128 dims (eight k-steps) without a read-ahead register set: at
+// two waves per SIMD the other wave covers the operand reads' latency.
+template <bool kSecond>
+__device__ __forceinline__ void duo_products(const uint16_t* ops, int e0, const bf16x8 (&qb)[8],
+                                             const bf16x8 (&q2h)[8], const bf16x8 (&q2l)[8],
+                                             f32x16& dmu, f32x16& dvar) {
+#pragma unroll
+  for (int dc = 0; dc < 8; ++dc) {
+    const int off = e0 ^ (dc << 4);
+    dmu = mfma32(as_bf16x8(*reinterpret_cast<const u32x4*>(ops + off)), qb[dc], dmu);
+    dmu = mfma32(as_bf16x8(*reinterpret_cast<const u32x4*>(ops + kSelPart + off)), qb[dc], dmu);
+    if constexpr (kSecond) {
+      const bf16x8 vh = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + 2 * kSelPart + off));
+      const bf16x8 vl = as_bf16x8(*reinterpret_cast<const u32x4*>(ops + 3 * kSelPart + off));
+      dvar = mfma32(vh, q2h[dc], dvar);
+      dvar = mfma32(vl, q2h[dc], dvar);
+      dvar = mfma32(vh, q2l[dc], dvar);
+    }
+  }
+}
+
+constexpr int kDuoThreads = 512;
+constexpr int kDuoMaxBlocks = 256;
+
+template <int SEL, int S>
+__global__ __launch_bounds__(kDuoThreads, 1) void selector_duo_kernel(SelArgs args) {
+  constexpr bool kSecond = SEL != SPX_SELECTOR_MEAN_BALANCED;
+  constexpr bool kDisp = SEL == SPX_SELECTOR_DISPERSION_MEAN;
+  constexpr int kParts = kSecond ? 4 : 2;
+
+  __shared__ __align__(16) uint16_t buf[2][kParts * kSelPart];
+  __shared__ __align__(16) uint16_t qbuf[2][kBlock * 128];  // tile t - it at qbuf[it]
+  __shared__ float log2_n[kDuoMaxBlocks];
+  __shared__ float log2_sigma[kDisp ? kDuoMaxBlocks : 1];
+  __shared__ float part[2][4][kDuoMaxBlocks];
+
+  // The two tiles' Q rows into qbuf (16-byte chunk c of row r at c ^ (r & 15));
+  // rows outside [0, seq) clamped (their registers are zeroed, or unused when
+  // t - 1 < 0).
+  auto dma_q2 = [&](const SelArgs& a, int t, int b, int h, int tid) {
+    const int w = tid >> 6;
+    const uint32_t lds_base =
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint16_t*)&qbuf[0][0];
+    const uint16_t* base = a.q + (int64_t)b * a.qs_b + (int64_t)h * a.qs_h;
+#pragma unroll
+    for (int i = 0; i < 2 * kBlock * 16 / kDuoThreads; ++i) {
+      const int p = i * kDuoThreads + tid;
+      const int it = p >> 11, r = (p >> 4) & 127, c = (p & 15) ^ (r & 15);
+      const int64_t row = max(0, min((t - it) * kBlock + r, a.seq - 1));
+      dma_gather16(base + row * a.qs_s + c * 8,
+                   lds_base + (uint32_t)(i * kDuoThreads + w * 64) * 16u);
+    }
+  };
+
+  {
+    const int tid = threadIdx.x;
+    for (int j = tid; j < args.blocks; j += kDuoThreads) log2_n[j] = log2f((float)args.counts[j]);
+    const int item = blockIdx.x;  // the host launches at most one workgroup per item
+    const int per_tile = args.batch * args.q_heads;
+    const int t = args.blocks - 1 - 2 * (item / per_tile), bh = item % per_tile;
+    const int b = bh / args.q_heads, h = bh % args.q_heads;
+    dma_q2(args, t, b, h, tid);
+    if (t > 0)
+      dma_chunk<kParts, kDuoThreads>(
+          args.ws + ((int64_t)b * args.kv_heads + h / (args.q_heads / args.kv_heads)) *
+                        args.chunks * kSelChunkElems,
+          buf[0], tid);
+  }
+  int slot = 0;  // buffer of the current item's first step
+
+  for (int item = blockIdx.x;; item += gridDim.x) {
+    // arguments re-read per item through an opaque pointer, the thread index through
+    // an opaque copy: nothing derived from them is held across items
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __attribute__((address_space(4))) SelArgs* ap =
+        (const __attribute__((address_space(4))) SelArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    const SelArgs a = *ap;
+#else
+    const SelArgs a = args;
+#endif
+    const int per_tile = a.batch * a.q_heads;
+    const int n_items = (a.blocks + 1) / 2 * per_tile;
+    if (item >= n_items) break;
+    const int tid = opaque((int)threadIdx.x), lane = tid & 63;
+    const int it = __builtin_amdgcn_readfirstlane(tid >> 8);  // tile t - it
+    const int w = (tid >> 6) & 3;                              // row group
+    const int col = lane & 31, half = lane >> 5;
+    const int group = a.q_heads / a.kv_heads;
+    const int64_t bg_elems = (int64_t)a.chunks * kSelChunkElems;
+    const SelConsts k{a.scale * kLog2e, 0.5f * a.scale * a.scale * kLog2e, a.scale * a.scale};
+    const int e0 = col * 128 + (((col >> 1) & 7) << 4) + ((half ^ (col & 1)) << 3);
+
+    const int t = a.blocks - 1 - 2 * (item / per_tile), bh = item % per_tile;
+    const int b = bh / a.q_heads, h = bh % a.q_heads, g = h / group;
+    const int tile = t - it;                                   // this wave's tile (-1: none)
+    const int nchunks = (t + kSelChunk - 1) / kSelChunk;       // the workgroup's steps: tile t
+    const int nstored = min(nchunks, S);
+    const int nsteps = nchunks + (nchunks - nstored);          // pass 1, then pass 2 past S
+    const int my_chunks = tile > 0 ? (tile + kSelChunk - 1) / kSelChunk : 0;
+    const uint16_t* src = a.ws + ((int64_t)b * a.kv_heads + g) * bg_elems;
+    const int next = item + gridDim.x;
+
+    auto issue_after = [&](int s) {
+      if (s + 1 < nsteps) {
+        const int s1 = s + 1;
+        const int jc = s1 < nchunks ? s1 : nstored + (s1 - nchunks);
+        dma_chunk<kParts, kDuoThreads>(src + (int64_t)jc * kSelChunkElems, buf[(slot + s1) & 1], tid);
+      }
+    };
+    auto issue_next_item = [&]() {
+      if (next < n_items) {
+        const int nt = a.blocks - 1 - 2 * (next / per_tile), nbh = next % per_tile;
+        const int nb = nbh / a.q_heads, nh = nbh % a.q_heads;
+        dma_q2(a, nt, nb, nh, tid);
+        if (nt > 0)
+          dma_chunk<kParts, kDuoThreads>(a.ws + ((int64_t)nb * a.kv_heads + nh / group) * bg_elems,
+                                         buf[(slot + nsteps) & 1], tid);
+      }
+    };
+    auto step_sync = [&]() {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      block_sync();
+    };
+
+    step_sync();  // Q and the first chunk landed; the previous item's LDS reads are done
+    const int64_t qrow = (int64_t)tile * kBlock + w * 32 + col;
+    const bool row_ok = tile >= 0 && qrow < a.seq;
+    bf16x8 qb[8], q2h[8], q2l[8];
+    read_q<kSecond, 128>(qbuf[it], w, col, half, row_ok, qb, q2h, q2l);
+    if (kDisp) {
+      for (int j = tid; j < t; j += kDuoThreads)
+        log2_sigma[j] = __log2f(a.sigma_v[((int64_t)b * a.blocks + j) * a.kv_heads + g]);
+    }
+    block_sync();  // the Q tiles are free for the next item's copy; log2_sigma visible
+    if (nsteps == 0) issue_next_item();
+
+    float m_run = -INFINITY, l_run = 0.0f;  // this lane's row state over its blocks
+    float st[S][16] = {};                    // logits of the stored chunks
+    f32x16 dmu = {}, dvar = {};
+
+    // ---- stored chunks: products, then the fold (the other tile's wave on the
+    // SIMD fills the matrix core meanwhile)
+#pragma unroll
+    for (int jc = 0; jc < S; ++jc) {
+      if (jc < nstored) {
+        if (jc > 0) step_sync();
+        issue_after(jc);
+        if (jc < my_chunks) {
+          dmu = f32x16{};
+          dvar = f32x16{};
+          duo_products<kSecond>(buf[(slot + jc) & 1], e0, qb, q2h, q2l, dmu, dvar);
+          float lg[16], val[16];
+          chunk_logits<kSecond, kDisp>(dmu, dvar, jc, tile, lane, log2_n, log2_sigma, k, lg, val);
+          fold_row(lg, m_run, l_run);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) st[jc][r] = kDisp ? val[r] : lg[r];
+        }
+      }
+    }
+    // ---- chunks past S, first pass: the row state only
+    for (int jc = S; jc < nchunks; ++jc) {
+      step_sync();
+      issue_after(jc);
+      if (jc < my_chunks) {
+        dmu = f32x16{};
+        dvar = f32x16{};
+        duo_products<kSecond>(buf[(slot + jc) & 1], e0, qb, q2h, q2l, dmu, dvar);
+        float lg[16], val[16];
+        chunk_logits<kSecond, kDisp>(dmu, dvar, jc, tile, lane, log2_n, log2_sigma, k, lg, val);
+        fold_row(lg, m_run, l_run);
+      }
+    }
+    if (nsteps == nchunks) issue_next_item();
+
+    // ---- the row's softmax maximum and sum: merge the two lane halves
+    float inv_l;
+    {
+      const float om = xor32(m_run), ol = xor32(l_run);
+      const float nm = fmaxf(m_run, om);
+      float nl = 0.0f;
+      if (nm != -INFINITY) {
+        nl = (m_run == -INFINITY ? 0.0f : l_run * exp2_fast(m_run - nm)) +
+             (om == -INFINITY ? 0.0f : ol * exp2_fast(om - nm));
+      }
+      m_run = nm;
+      // rows past the sequence end contribute nothing
+      inv_l = (nl > 0.0f && row_ok) ? 1.0f / nl : 0.0f;
+    }
+#pragma unroll
+    for (int jc = 0; jc < S; ++jc) {
+      if (jc < nstored && jc < my_chunks) {
+        float v[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[r] = st[jc][r];
+        chunk_sums(v, m_run, inv_l, jc, w, lane, part[it]);
+      }
+    }
+    // ---- chunks past S, second pass: products again, then their sums
+    for (int jc = nstored; jc < nchunks; ++jc) {
+      const int sc = nchunks + (jc - nstored);
+      step_sync();
+      issue_after(sc);
+      if (jc < my_chunks) {
+        dmu = f32x16{};
+        dvar = f32x16{};
+        duo_products<kSecond>(buf[(slot + sc) & 1], e0, qb, q2h, q2l, dmu, dvar);
+        float lg[16], val[16];
+        chunk_logits<kSecond, kDisp>(dmu, dvar, jc, tile, lane, log2_n, log2_sigma, k, lg, val);
+        if constexpr (kDisp) chunk_sums(val, m_run, inv_l, jc, w, lane, part[it]);
+        else chunk_sums(lg, m_run, inv_l, jc, w, lane, part[it]);
+      }
+    }
+    if (nsteps > nchunks) issue_next_item();
+
+    block_sync();  // every wave's block sums are in part
+    {
+      // thread (tile t - i, block j): i = tid / 256, j = tid % 256 (blocks <= 256)
+      const int i = tid >> 8, j = tid & 255, tt = t - i;
+      if (tt >= 0 && j < a.blocks) {
+        const float inv_rows = 1.0f / (float)min(kBlock, a.seq - tt * kBlock);
+        const float sc = j < tt ? (part[i][0][j] + part[i][1][j] + part[i][2][j] + part[i][3][j]) * inv_rows
+                                : 0.0f;
+        a.score[b * a.ss_b + tt * a.ss_t + j * a.ss_j + h * a.ss_h] = sc;
+      }
+    }
+    slot = (slot + nsteps) & 1;
+  }
+}
+
 }  // namespace spx
 
 using namespace spx;
@@ -1173,13 +1420,18 @@ int run_selectors(const void* q, const int64_t* q_strides, const float* mean_k,
   a.ss_h = score_strides[3];
   const int64_t items = (int64_t)blocks * batch * q_heads;
   const unsigned grid = (unsigned)std::min<int64_t>(items, cu_count());
-  // Up to 8 chunks (256 blocks) at head_dim 128: the two-waves-per-SIMD kernel,
-  // which keeps every chunk's logits in registers. Longer rows and head_dim 256:
-  // the one-wave-per-SIMD kernel, its logits of sel_store(...) chunks in AGPRs and
-  // the products of the rest formed twice (on 131072-token rows it ran 5.0-5.3 ms
-  // per cgf_mean layer against 5.6 ms for the pair kernel with its unstored chunks
-  // in two-barrier steps).
+  // Up to 8 chunks (256 blocks) at head_dim 128: mean_balanced in the duo kernel
+  // (two tiles per workgroup, every chunk's logits in registers: 0.155 ms at 32K
+  // against 0.211 ms in the pair kernel), cgf_mean and dispersion_mean in the pair
+  // kernel (the q*q split leaves the duo kernel room for 3 chunks only, and the
+  // products formed twice for the rest made it no faster: 0.308 / 0.369 ms against
+  // 0.304 / 0.347 ms). Longer rows and head_dim 256: the one-wave-per-SIMD kernel,
+  // its logits of sel_store(...) chunks in AGPRs and the products of the rest formed
+  // twice (on 131072-token rows it ran 5.0-5.3 ms per cgf_mean layer against 5.6 ms
+  // for the pair kernel with its unstored chunks in two-barrier steps).
   const bool long_rows = chunks > 8;
+  const unsigned duo_grid =
+      (unsigned)std::min<int64_t>((int64_t)(blocks + 1) / 2 * batch * q_heads, cu_count());
   switch (selector * 1000 + head_dim * 2 + (long_rows ? 1 : 0)) {
 #define SPX_SEL_CASE(SEL, D)                                                      \
   case SEL * 1000 + D * 2 + 1:                                                    \
@@ -1193,7 +1445,9 @@ int run_selectors(const void* q, const int64_t* q_strides, const float* mean_k,
   case SEL * 1000 + 512:                                                          \
     selector_kernel<SEL, 256, sel_store(SEL, 256, false)><<<grid, kSelThreads, 0, st>>>(a); \
     break;
-    SPX_PAIR_CASE(SPX_SELECTOR_MEAN_BALANCED)
+    case SPX_SELECTOR_MEAN_BALANCED * 1000 + 256:
+      selector_duo_kernel<SPX_SELECTOR_MEAN_BALANCED, 8><<<duo_grid, kDuoThreads, 0, st>>>(a);
+      break;
     SPX_PAIR_CASE(SPX_SELECTOR_CGF_MEAN)
     SPX_PAIR_CASE(SPX_SELECTOR_DISPERSION_MEAN)
     SPX_SEL_CASE(SPX_SELECTOR_MEAN_BALANCED, 128)
