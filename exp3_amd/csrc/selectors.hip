@@ -335,6 +335,37 @@ __device__ __forceinline__ void read_q(const uint16_t* qbuf, int w, int col, int
   }
 }
 
+// Persistent item deal. Items are (rank, bh): rank 0 the heaviest tile (or tile
+// pair), bh = batch * Hq + head. Workgroup w runs on XCD w % 8 (the hardware deals
+// workgroup ids round robin over the 8 XCDs; the grid is a multiple of 8); the
+// workgroups of XCD x take the ranks x, x + 8, x + 16, ... with all their heads, in
+// turn. All heads of a rank thus run on one XCD, so the partial cache lines of the
+// head-interleaved score rows ([B, NB, NB, Hq], 4 bytes per head) meet in one L2
+// instead of leaving it as 32-byte partial writes from every XCD. Returns the m-th
+// item of workgroup w (an index >= ranks * per_rank once the ranks are used up).
+__device__ __forceinline__ int xcd_item(int w, int m, int nwg, int per_rank) {
+  const int x = w & 7, k = w >> 3, per_xcd = nwg >> 3;
+  const int idx = k + m * per_xcd;
+  return (x + 8 * (idx / per_rank)) * per_rank + idx % per_rank;
+}
+
+// The deal of the long-row kernel when the B * Hkv (batch, kv group) streams divide
+// the 8 XCDs: stream s runs on XCDs s X .. s X + X - 1 (X = 8 / streams), which
+// take its ranks in turn (rank u, u + X, ... on the stream's u-th XCD) with the
+// group's heads. An XCD then holds one stream's descriptor chunks in its L2
+// (1 MB per stream at 131072 tokens) instead of every stream's. Returns the item
+// (rank * per_rank + b * Hq + head) or an index >= ranks * per_rank when done.
+__device__ __forceinline__ int xcd_item_stream(int w, int m, int nwg, int streams, int group,
+                                               int kv_heads, int q_heads, int ranks) {
+  const int x = w & 7, k = w >> 3, per_xcd = nwg >> 3;
+  const int X = 8 / streams, st = x / X, u = x % X;
+  const int idx = k + m * per_xcd;
+  const int rank = u + X * (idx / group);
+  if (rank >= ranks) return ranks * q_heads * (streams / kv_heads);
+  const int b = st / kv_heads, g = st % kv_heads;
+  return rank * (q_heads * (streams / kv_heads)) + b * q_heads + g * group + idx % group;
+}
+
 // A value parked in an accumulation register (AGPR) until the end of the item:
 // the kernel's MFMAs use VGPR accumulators, so the AGPR file holds the logits of
 // the stored chunks.
@@ -484,20 +515,26 @@ __global__ __launch_bounds__(kSelThreads, 1) void selector_kernel(SelArgs args) 
   {
     const int tid = threadIdx.x;
     for (int j = tid; j < args.blocks; j += kSelThreads) log2_n[j] = log2f((float)args.counts[j]);
-    const int item = blockIdx.x;  // the host launches at most one workgroup per item
     const int per_tile = args.batch * args.q_heads;
-    const int t = args.blocks - 1 - item / per_tile, bh = item % per_tile;
-    const int b = bh / args.q_heads, h = bh % args.q_heads;
-    dma_q<D>(args, t, b, h, qbuf, tid);
-    if (t > 0) {
-      const int64_t bg_elems = (int64_t)args.chunks * kHalves * kSelChunkElems;
-      dma_chunk<kParts>(args.ws + ((int64_t)b * args.kv_heads + h / (args.q_heads / args.kv_heads)) * bg_elems,
-                        buf[0], tid);
+    const int streams = args.batch * args.kv_heads;
+    const int item = 8 % streams == 0
+        ? xcd_item_stream(blockIdx.x, 0, gridDim.x, streams, args.q_heads / args.kv_heads,
+                          args.kv_heads, args.q_heads, args.blocks)
+        : xcd_item(blockIdx.x, 0, gridDim.x, per_tile);
+    if (item < args.blocks * per_tile) {
+      const int t = args.blocks - 1 - item / per_tile, bh = item % per_tile;
+      const int b = bh / args.q_heads, h = bh % args.q_heads;
+      dma_q<D>(args, t, b, h, qbuf, tid);
+      if (t > 0) {
+        const int64_t bg_elems = (int64_t)args.chunks * kHalves * kSelChunkElems;
+        dma_chunk<kParts>(args.ws + ((int64_t)b * args.kv_heads + h / (args.q_heads / args.kv_heads)) * bg_elems,
+                          buf[0], tid);
+      }
     }
   }
   int slot = 0;  // buffer of the current item's first step
 
-  for (int item = blockIdx.x;; item += gridDim.x) {
+  for (int m = 0;; ++m) {
     // The arguments are read afresh for every item through an opaque pointer and the
     // thread index through an opaque copy, so nothing derived from them is held in
     // registers across items.
@@ -511,6 +548,14 @@ __global__ __launch_bounds__(kSelThreads, 1) void selector_kernel(SelArgs args) 
 #endif
     const int per_tile = a.batch * a.q_heads;
     const int n_items = a.blocks * per_tile;
+    const int streams = a.batch * a.kv_heads;
+    const bool by_stream = 8 % streams == 0;
+    auto deal = [&](int mm) {
+      return by_stream ? xcd_item_stream(blockIdx.x, mm, gridDim.x, streams,
+                                         a.q_heads / a.kv_heads, a.kv_heads, a.q_heads, a.blocks)
+                       : xcd_item(blockIdx.x, mm, gridDim.x, per_tile);
+    };
+    const int item = deal(m);
     if (item >= n_items) break;
     const int tid = opaque((int)threadIdx.x), lane = tid & 63, w = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
@@ -528,7 +573,7 @@ __global__ __launch_bounds__(kSelThreads, 1) void selector_kernel(SelArgs args) 
     const int p1 = nchunks * kHalves;                     // first-pass (chunk, half) steps
     const int nsteps = p1 + (nchunks - nstored) * kHalves;
     const uint16_t* src = a.ws + ((int64_t)b * a.kv_heads + g) * bg_elems;
-    const int next = item + gridDim.x;
+    const int next = deal(m + 1);
 
     // Copy what step s + 1 reads into its buffer: this item's next (chunk, half),
     // or after the last step the next item's Q tile and first step. Called after
@@ -827,7 +872,7 @@ __device__ __forceinline__ void pair_waves(const SelArgs& args, const PairLds& L
   constexpr int kParts = kSecond ? 4 : 2;
   int slot = 0;  // buffer of the current item's first step
 
-  for (int item = blockIdx.x;; item += gridDim.x) {
+  for (int m = 0;; ++m) {
     // arguments re-read per item through an opaque pointer, the thread index through
     // an opaque copy: nothing derived from them is held across items
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -840,6 +885,7 @@ __device__ __forceinline__ void pair_waves(const SelArgs& args, const PairLds& L
 #endif
     const int per_tile = a.batch * a.q_heads;
     const int n_items = a.blocks * per_tile;
+    const int item = xcd_item(blockIdx.x, m, gridDim.x, per_tile);
     if (item >= n_items) break;
     const int tid = opaque((int)threadIdx.x), lane = tid & 63;
     const int rg = (tid >> 6) & 3;  // row group
@@ -855,7 +901,7 @@ __device__ __forceinline__ void pair_waves(const SelArgs& args, const PairLds& L
     const int nstored = min(nchunks, S);
     const int nsteps = nchunks + (nchunks - nstored);     // pass 1, then pass 2 past S
     const uint16_t* src = a.ws + ((int64_t)b * a.kv_heads + g) * bg_elems;
-    const int next = item + gridDim.x;
+    const int next = xcd_item(blockIdx.x, m + 1, gridDim.x, per_tile);
 
     // Copy this item's step s + 1 into its buffer; called after the barrier that
     // opens step s, when every wave is done with step s - 1.
@@ -1075,16 +1121,18 @@ __global__ __launch_bounds__(kPairThreads, 1) void selector_pair_kernel(SelArgs 
   {
     const int tid = threadIdx.x;
     for (int j = tid; j < args.blocks; j += kPairThreads) log2_n[j] = log2f((float)args.counts[j]);
-    const int item = blockIdx.x;  // the host launches at most one workgroup per item
     const int per_tile = args.batch * args.q_heads;
-    const int t = args.blocks - 1 - item / per_tile, bh = item % per_tile;
-    const int b = bh / args.q_heads, h = bh % args.q_heads;
-    dma_q<128, kPairThreads>(args, t, b, h, qbuf, tid);
-    if (t > 0) {
-      const int64_t bg_elems = (int64_t)args.chunks * kSelChunkElems;
-      dma_chunk<kParts, kPairThreads>(
-          args.ws + ((int64_t)b * args.kv_heads + h / (args.q_heads / args.kv_heads)) * bg_elems,
-          buf[0], tid);
+    const int item = xcd_item(blockIdx.x, 0, gridDim.x, per_tile);
+    if (item < args.blocks * per_tile) {
+      const int t = args.blocks - 1 - item / per_tile, bh = item % per_tile;
+      const int b = bh / args.q_heads, h = bh % args.q_heads;
+      dma_q<128, kPairThreads>(args, t, b, h, qbuf, tid);
+      if (t > 0) {
+        const int64_t bg_elems = (int64_t)args.chunks * kSelChunkElems;
+        dma_chunk<kParts, kPairThreads>(
+            args.ws + ((int64_t)b * args.kv_heads + h / (args.q_heads / args.kv_heads)) * bg_elems,
+            buf[0], tid);
+      }
     }
   }
   if (__builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8) == 0) pair_waves<SEL, S, 0>(args, L);
@@ -1159,20 +1207,22 @@ __global__ __launch_bounds__(kDuoThreads, 1) void selector_duo_kernel(SelArgs ar
   {
     const int tid = threadIdx.x;
     for (int j = tid; j < args.blocks; j += kDuoThreads) log2_n[j] = log2f((float)args.counts[j]);
-    const int item = blockIdx.x;  // the host launches at most one workgroup per item
     const int per_tile = args.batch * args.q_heads;
-    const int t = args.blocks - 1 - 2 * (item / per_tile), bh = item % per_tile;
-    const int b = bh / args.q_heads, h = bh % args.q_heads;
-    dma_q2(args, t, b, h, tid);
-    if (t > 0)
-      dma_chunk<kParts, kDuoThreads>(
-          args.ws + ((int64_t)b * args.kv_heads + h / (args.q_heads / args.kv_heads)) *
-                        args.chunks * kSelChunkElems,
-          buf[0], tid);
+    const int item = xcd_item(blockIdx.x, 0, gridDim.x, per_tile);
+    if (item < (args.blocks + 1) / 2 * per_tile) {
+      const int t = args.blocks - 1 - 2 * (item / per_tile), bh = item % per_tile;
+      const int b = bh / args.q_heads, h = bh % args.q_heads;
+      dma_q2(args, t, b, h, tid);
+      if (t > 0)
+        dma_chunk<kParts, kDuoThreads>(
+            args.ws + ((int64_t)b * args.kv_heads + h / (args.q_heads / args.kv_heads)) *
+                          args.chunks * kSelChunkElems,
+            buf[0], tid);
+    }
   }
   int slot = 0;  // buffer of the current item's first step
 
-  for (int item = blockIdx.x;; item += gridDim.x) {
+  for (int m = 0;; ++m) {
     // arguments re-read per item through an opaque pointer, the thread index through
     // an opaque copy: nothing derived from them is held across items
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -1185,6 +1235,7 @@ __global__ __launch_bounds__(kDuoThreads, 1) void selector_duo_kernel(SelArgs ar
 #endif
     const int per_tile = a.batch * a.q_heads;
     const int n_items = (a.blocks + 1) / 2 * per_tile;
+    const int item = xcd_item(blockIdx.x, m, gridDim.x, per_tile);
     if (item >= n_items) break;
     const int tid = opaque((int)threadIdx.x), lane = tid & 63;
     const int it = __builtin_amdgcn_readfirstlane(tid >> 8);  // tile t - it
@@ -1203,7 +1254,7 @@ __global__ __launch_bounds__(kDuoThreads, 1) void selector_duo_kernel(SelArgs ar
     const int nsteps = nchunks + (nchunks - nstored);          // pass 1, then pass 2 past S
     const int my_chunks = tile > 0 ? (tile + kSelChunk - 1) / kSelChunk : 0;
     const uint16_t* src = a.ws + ((int64_t)b * a.kv_heads + g) * bg_elems;
-    const int next = item + gridDim.x;
+    const int next = xcd_item(blockIdx.x, m + 1, gridDim.x, per_tile);
 
     auto issue_after = [&](int s) {
       if (s + 1 < nsteps) {
@@ -1418,8 +1469,14 @@ int run_selectors(const void* q, const int64_t* q_strides, const float* mean_k,
   a.score = score;
   a.ss_b = score_strides[0]; a.ss_t = score_strides[1]; a.ss_j = score_strides[2];
   a.ss_h = score_strides[3];
+  // persistent grids: a multiple of 8 workgroups (xcd_item), at most one per CU
+  // and at most one per item rounded up to 8 (the spare ones find no item and exit)
   const int64_t items = (int64_t)blocks * batch * q_heads;
-  const unsigned grid = (unsigned)std::min<int64_t>(items, cu_count());
+  auto grid_for = [](int64_t n) {
+    const int64_t cus = std::max<int64_t>(8, cu_count() / 8 * 8);
+    return (unsigned)std::min<int64_t>(cus, (n + 7) / 8 * 8);
+  };
+  const unsigned grid = grid_for(items);
   // Up to 8 chunks (256 blocks) at head_dim 128: mean_balanced in the duo kernel
   // (two tiles per workgroup, every chunk's logits in registers: 0.155 ms at 32K
   // against 0.211 ms in the pair kernel), cgf_mean and dispersion_mean in the pair
@@ -1430,8 +1487,7 @@ int run_selectors(const void* q, const int64_t* q_strides, const float* mean_k,
   // twice (on 131072-token rows it ran 5.0-5.3 ms per cgf_mean layer against 5.6 ms
   // for the pair kernel with its unstored chunks in two-barrier steps).
   const bool long_rows = chunks > 8;
-  const unsigned duo_grid =
-      (unsigned)std::min<int64_t>((int64_t)(blocks + 1) / 2 * batch * q_heads, cu_count());
+  const unsigned duo_grid = grid_for((int64_t)(blocks + 1) / 2 * batch * q_heads);
   switch (selector * 1000 + head_dim * 2 + (long_rows ? 1 : 0)) {
 #define SPX_SEL_CASE(SEL, D)                                                      \
   case SEL * 1000 + D * 2 + 1:                                                    \
