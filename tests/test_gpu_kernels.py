@@ -283,6 +283,34 @@ def test_selector_scores(gpu, length, selector):
     np.testing.assert_allclose(actual, expected, atol=2e-5, rtol=2e-5)   # check_math.py:287-290
 
 
+# (batch, q heads, kv heads, head dim, length): the selector kernels deal whole tiles to
+# XCDs, and the long-row / d=256 kernel one (batch, kv group) stream per XCD pair when
+# the streams divide 8, else whole tiles. 40000 tokens (313 blocks) takes d=128 to the
+# long-row kernel; layouts with 3, 6 and 9 streams take the whole-tile deal there.
+SELECTOR_LAYOUTS = [(1, 6, 3, 128, 40000), (3, 4, 2, 128, 1089), (1, 6, 3, 256, 1089),
+                    (3, 6, 3, 256, 600), (2, 8, 2, 128, 40000)]
+
+
+@pytest.mark.parametrize("batch,q_heads,kv_heads,head_dim,length", SELECTOR_LAYOUTS)
+@pytest.mark.parametrize("selector", ("mean_balanced", "cgf_mean", "dispersion_mean"))
+def test_selector_scores_layouts(gpu, selector, batch, q_heads, kv_heads, head_dim, length):
+    q, k, v, _ = synthetic.make_inputs(length, seed=29, q_heads=q_heads, kv_heads=kv_heads,
+                                       head_dim=head_dim, batch=batch)
+    qg, kg, vg = _gpu(q, k, v)
+    desc = kernels.block_descriptors(kg, vg)
+    scale = head_dim ** -0.5
+    actual = to_np(kernels.selector_scores(qg, desc, scale, selector))
+    e_desc = ref.BlockDescriptors(*(to_np(getattr(desc, n)) for n in
+                                    ("mean_k", "mean_v", "var_k", "sigma_v", "counts")))
+    blocks = ref.num_blocks(length)
+    # long sequences: the oracle scores sampled tiles (first, middle, the last two)
+    tiles = None if blocks <= 40 else [1, blocks // 2, blocks - 2, blocks - 1]
+    expected = ref.selector_scores(to_np(q), e_desc, scale, selector, tiles=tiles)
+    if tiles is not None:
+        actual, expected = actual[:, tiles], expected[:, tiles]
+    np.testing.assert_allclose(actual, expected, atol=2e-5, rtol=2e-5)   # check_math.py:287-290
+
+
 @pytest.mark.parametrize("selector", ("mean_balanced", "cgf_mean", "dispersion_mean"))
 def test_selector_scores_full_size_repeatable(gpu, selector):
     """S=32640 (255 tiles, 8 chunks of 32 blocks): every call gives the same bits,
