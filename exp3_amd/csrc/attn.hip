@@ -800,9 +800,11 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
   const bool live = t >= 0;
 
   copy_q(a, b, h, t_item[0], kbuf[1], vbuf[1], tid);   // read after the list phase
-  // Both items' list counts and entries are loaded now, with the Q copy in flight: every
-  // position a list row holds (NB) is read (rows and positions clamped into range, so
-  // no branch separates the loads), and those at or past the count are dropped.
+  // Both items' list counts and entries are loaded now, with the Q copy in flight. Each
+  // thread reads its positions of the row clamped to the last counted one (rows and
+  // positions clamped into range, so no branch separates the loads): positions past
+  // the count re-read that entry's cache line instead of fetching the rest of the row
+  // (heads interleave, so each position is its own line), and are dropped below.
   int count_of[2] = {0, 0};
   int64_t entry[2][kListLoads];
   if (a.idx) {
@@ -811,9 +813,10 @@ __device__ __forceinline__ void attn_item(const AttnArgs& a, int pair, int hg) {
       const int tt = max(t_item[it], 0);
       count_of[it] = a.cnt[b * a.cs_b + tt * a.cs_t + h * a.cs_h];
       const int64_t* list = a.idx + b * a.is_b + tt * a.is_t + h * a.is_h;
+      const int last = min(max(count_of[it], 1), a.blocks) - 1;
 #pragma unroll
       for (int r = 0; r < kListLoads; ++r)
-        entry[it][r] = list[min(tid + r * kAttnThreads, a.blocks - 1) * a.is_p];
+        entry[it][r] = list[min(tid + r * kAttnThreads, last) * a.is_p];
     }
   }
   WaveState ws;
