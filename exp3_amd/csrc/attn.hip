@@ -450,18 +450,14 @@ __device__ __forceinline__ void shift_and_check(f32x16& sv, WaveState& ws, float
   }
 }
 
-// acc + lo + hi of a packed bf16 pair (v_dot2_f32_bf16 with (1, 1); issued from
-// assembly because the compiler's dot2 builtin lowering reads the wrong register
-// when several of them are chained)
-__device__ __forceinline__ float add_bf16_pair(float acc, uint32_t pair) {
-  asm("v_dot2_f32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(pair), "s"(0x3f803f80u));
-  return acc;
-}
-
 // probabilities of one sub-block (shifted scores x) as bf16 B operands; the
-// running sum adds the rounded values (the ones the P V product uses)
+// running sum adds the fp32 probabilities, as upstream/flashprefill_native_forward.py
+// :332-338 does (sum before the cast for the P V product), pairwise so that the
+// chain into l is short. (Summing the packed bf16 pairs with v_dot2_f32_bf16 instead
+// took issue cycles from the matrix products beside it: four per product halved
+// their rate in a microbenchmark, while plain adds there were nearly free.)
 __device__ __forceinline__ void sub_exp(const f32x16& xv, WaveState& ws, bf16x8 (&p)[2]) {
-  float l = ws.l;
+  float pair_sum[8];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     u32x4 w;
@@ -470,11 +466,13 @@ __device__ __forceinline__ void sub_exp(const f32x16& xv, WaveState& ws, bf16x8 
       const float a = exp2_fast(xv[8 * h + 2 * i]);
       const float b = exp2_fast(xv[8 * h + 2 * i + 1]);
       w[i] = pack_bf16x2(a, b);
-      l = add_bf16_pair(l, w[i]);
+      pair_sum[4 * h + i] = a + b;
     }
     p[h] = as_bf16x8(w);
   }
-  ws.l = l;
+  const float sum = ((pair_sum[0] + pair_sum[1]) + (pair_sum[2] + pair_sum[3])) +
+                    ((pair_sum[4] + pair_sum[5]) + (pair_sum[6] + pair_sum[7]));
+  ws.l += sum;
 }
 
 // The copy of the next block: source tiles and the other buffers.

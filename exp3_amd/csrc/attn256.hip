@@ -41,14 +41,6 @@ constexpr int kA2MaxBlocks = 1024;
 constexpr float kLazy = 64.0f;             // log2 headroom before a column's running max moves
                                            // (bf16 P, fp32 O and l: 2^64 loses nothing)
 
-// acc + lo + hi of a packed bf16 pair (v_dot2_f32_bf16 with (1, 1), from assembly:
-// the compiler's dot2 builtin lowering reads the wrong register when several of
-// them are chained)
-__device__ __forceinline__ float add_bf16_pair(float acc, uint32_t pair) {
-  asm("v_dot2_f32_bf16 %0, %1, %2, %0" : "+v"(acc) : "v"(pair), "s"(0x3f803f80u));
-  return acc;
-}
-
 struct Attn256Args {
   const uint16_t* q;
   int64_t qs_b, qs_s, qs_h;
@@ -117,15 +109,23 @@ __device__ __forceinline__ void softmax_pv(f32x16& x, const uint16_t* vb, f32x16
 #pragma unroll
     for (int r = 0; r < 16; ++r) x[r] -= d;
   }
-  // probabilities as bf16 B operands; the running sum adds the rounded values
+  // probabilities as bf16 B operands; the running sum adds the fp32 probabilities
+  // (upstream/flashprefill_native_forward.py:332-338), pairwise: plain adds run
+  // beside the matrix products almost for free, v_dot2_f32_bf16 sums of the packed
+  // pairs did not
   u32x4 pb0, pb1;
+  float pair_sum[8];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    pb0[e] = pack_bf16x2(exp2_fast(x[2 * e]), exp2_fast(x[2 * e + 1]));
-    l = add_bf16_pair(l, pb0[e]);
-    pb1[e] = pack_bf16x2(exp2_fast(x[8 + 2 * e]), exp2_fast(x[8 + 2 * e + 1]));
-    l = add_bf16_pair(l, pb1[e]);
+    const float a0 = exp2_fast(x[2 * e]), b0 = exp2_fast(x[2 * e + 1]);
+    const float a1 = exp2_fast(x[8 + 2 * e]), b1 = exp2_fast(x[8 + 2 * e + 1]);
+    pb0[e] = pack_bf16x2(a0, b0);
+    pb1[e] = pack_bf16x2(a1, b1);
+    pair_sum[e] = a0 + b0;
+    pair_sum[4 + e] = a1 + b1;
   }
+  l += ((pair_sum[0] + pair_sum[1]) + (pair_sum[2] + pair_sum[3])) +
+       ((pair_sum[4] + pair_sum[5]) + (pair_sum[6] + pair_sum[7]));
 #pragma unroll
   for (int d2 = 0; d2 < 4; ++d2) {
     bf16x8 vr[4];
