@@ -112,14 +112,16 @@ def test_exact_attention_sparse_vs_oracle(gpu, length):
 def test_exact_attention_list_edge_cases(gpu):
     """As in the reference: a listed future block is attended without a mask (only
     the diagonal block is masked), ids outside [0, NB) are skipped (also those whose
-    low 32 bits are in range), and a count of 0 gives output 0 and LSE -inf."""
+    low 32 bits are in range), a block listed n times is attended n times (here by
+    both tiles of the pair (4, 3), twice and three times), and a count of 0 gives
+    output 0 and LSE -inf."""
     length = 1089
     q, k, v = qkv(length, seed=11)
     blocks = ref.num_blocks(length)
     idx, cnt = ref.indices_from_mask(_sparse_selection(length, seed=5))
     idx, cnt = idx.copy(), cnt.copy()
     for t, h, j in ((3, 0, 5), (4, 2, blocks + 3), (6, 3, -1), (7, 4, (1 << 32) + 2),
-                    (8, 5, -(1 << 32) + 3)):
+                    (8, 5, -(1 << 32) + 3), (4, 6, 0), (3, 6, 0), (3, 6, 0)):
         idx[0, t, cnt[0, t, h], h] = j
         cnt[0, t, h] += 1
     cnt[0, 5, 1] = 0
