@@ -287,8 +287,11 @@ def test_selector_scores(gpu, length, selector):
 # XCDs, and the long-row / d=256 kernel one (batch, kv group) stream per XCD pair when
 # the streams divide 8, else whole tiles. 40000 tokens (313 blocks) takes d=128 to the
 # long-row kernel; layouts with 3, 6 and 9 streams take the whole-tile deal there.
+# 32768 tokens (256 blocks) is the longest row of the short-row kernels (8 chunks, the
+# last tile's last chunk 31 blocks), 32769 (257 blocks) the shortest of the long-row kernel.
 SELECTOR_LAYOUTS = [(1, 6, 3, 128, 40000), (3, 4, 2, 128, 1089), (1, 6, 3, 256, 1089),
-                    (3, 6, 3, 256, 600), (2, 8, 2, 128, 40000)]
+                    (3, 6, 3, 256, 600), (2, 8, 2, 128, 40000), (1, 4, 2, 128, 32768),
+                    (1, 4, 2, 128, 32769)]
 
 
 @pytest.mark.parametrize("batch,q_heads,kv_heads,head_dim,length", SELECTOR_LAYOUTS)
