@@ -145,6 +145,8 @@ def test_kernel_view_keeps_transposed_layout():
     assert _lib.kernel_view(strided).stride()[-1] == 1
     with pytest.raises(ValueError):
         _lib.kernel_view(torch.zeros(1, 8, 1, 128))
+    with pytest.raises(ValueError, match="bfloat16"):   # the kernels read bf16 only
+        _lib.kernel_view(torch.zeros(1, 8, 1, 128, dtype=torch.float16))
 
 
 def test_rope_matches_transformers_qwen2():
