@@ -493,3 +493,36 @@ def test_selection_accounting(gpu):
             assert got == pytest.approx(value, rel=1e-12), key
         else:
             assert got == value, key
+
+
+@pytest.mark.parametrize("length,seed", [(1089, 101), (4096, 103)])
+def test_exact_attention_random_unsorted_lists(gpu, length, seed):
+    """Seeded random lists: for every (tile, head) a random subset of the causal
+    blocks 0..t in random order, some entries repeated, a random count, and garbage
+    (out-of-range and negative ids) past the count, which must be ignored. The
+    kernel merges each tile pair's lists into one ascending walk; the result must
+    match the oracle's walk of the lists as given."""
+    q, k, v = inputs(length, seed=seed)
+    qg, kg, vg = _gpu(q, k, v)
+    blocks = ref.num_blocks(length)
+    rng = np.random.default_rng(seed)
+    idx = rng.integers(-3 * blocks, 3 * blocks, size=(1, blocks, blocks, 28)).astype(np.int64)
+    cnt = np.zeros((1, blocks, 28), np.int32)
+    for t in range(blocks):
+        for h in range(28):
+            keep = rng.permutation(t + 1)[: rng.integers(0, t + 2)]
+            extra = rng.choice(keep, size=min(len(keep), blocks - len(keep), rng.integers(0, 3)),
+                               replace=False) if len(keep) else np.array([], np.int64)
+            row = rng.permutation(np.concatenate([keep, extra]).astype(np.int64))
+            assert len(row) <= blocks
+            idx[0, t, : len(row), h] = row
+            cnt[0, t, h] = len(row)
+    out, lse = up.exact_attention(qg, kg, vg, torch.from_numpy(idx).cuda(),
+                                  torch.from_numpy(cnt).cuda(), SCALE)
+    e_out, e_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE)
+    a_out, a_lse = to_np(out), to_np(lse)
+    assert_output_close(a_out, e_out, what="random unsorted lists")
+    finite = np.isfinite(e_lse)
+    np.testing.assert_array_equal(np.isfinite(a_lse), finite)
+    np.testing.assert_allclose(a_lse[finite], e_lse[finite], atol=0.02, rtol=0.01)
+    assert (a_out[~finite] == 0).all()
