@@ -495,21 +495,15 @@ def test_selection_accounting(gpu):
             assert got == value, key
 
 
-@pytest.mark.parametrize("length,seed", [(1089, 101), (4096, 103)])
-def test_exact_attention_random_unsorted_lists(gpu, length, seed):
-    """Seeded random lists: for every (tile, head) a random subset of the causal
-    blocks 0..t in random order, some entries repeated, a random count, and garbage
-    (out-of-range and negative ids) past the count, which must be ignored. The
-    kernel merges each tile pair's lists into one ascending walk; the result must
-    match the oracle's walk of the lists as given."""
-    q, k, v = inputs(length, seed=seed)
-    qg, kg, vg = _gpu(q, k, v)
-    blocks = ref.num_blocks(length)
+def _random_lists(blocks, seed, heads=28):
+    """For every (tile, head) a random subset of the causal blocks 0..t in random
+    order, some entries repeated, a random count (empty rows included), and garbage
+    (out-of-range and negative ids) past the count."""
     rng = np.random.default_rng(seed)
-    idx = rng.integers(-3 * blocks, 3 * blocks, size=(1, blocks, blocks, 28)).astype(np.int64)
-    cnt = np.zeros((1, blocks, 28), np.int32)
+    idx = rng.integers(-3 * blocks, 3 * blocks, size=(1, blocks, blocks, heads)).astype(np.int64)
+    cnt = np.zeros((1, blocks, heads), np.int32)
     for t in range(blocks):
-        for h in range(28):
+        for h in range(heads):
             keep = rng.permutation(t + 1)[: rng.integers(0, t + 2)]
             extra = rng.choice(keep, size=min(len(keep), blocks - len(keep), rng.integers(0, 3)),
                                replace=False) if len(keep) else np.array([], np.int64)
@@ -517,6 +511,17 @@ def test_exact_attention_random_unsorted_lists(gpu, length, seed):
             assert len(row) <= blocks
             idx[0, t, : len(row), h] = row
             cnt[0, t, h] = len(row)
+    return idx, cnt
+
+
+@pytest.mark.parametrize("length,seed", [(1089, 101), (4096, 103)])
+def test_exact_attention_random_unsorted_lists(gpu, length, seed):
+    """Seeded random lists (``_random_lists``), which must be walked as given: the
+    kernel merges each tile pair's lists into one ascending walk and ignores the
+    entries past each count; the result must match the oracle's walk of the lists."""
+    q, k, v = inputs(length, seed=seed)
+    qg, kg, vg = _gpu(q, k, v)
+    idx, cnt = _random_lists(ref.num_blocks(length), seed)
     out, lse = up.exact_attention(qg, kg, vg, torch.from_numpy(idx).cuda(),
                                   torch.from_numpy(cnt).cuda(), SCALE)
     e_out, e_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE)
@@ -526,3 +531,31 @@ def test_exact_attention_random_unsorted_lists(gpu, length, seed):
     np.testing.assert_array_equal(np.isfinite(a_lse), finite)
     np.testing.assert_allclose(a_lse[finite], e_lse[finite], atol=0.02, rtol=0.01)
     assert (a_out[~finite] == 0).all()
+
+
+@pytest.mark.parametrize("length,seed", [(1089, 107), (4096, 109)])
+def test_sparse_attention_mean_random_lists(gpu, length, seed):
+    """The fused mean-method launch (exact blocks + block-mean tail in one softmax)
+    on the same kind of random lists: the tail is every causal block j < t the row
+    does not list, whatever the order and repeats of the listed ones; against the
+    oracle's exact part, mean tail and logaddexp merge (kernels.py:179-230, 312-325)."""
+    q, k, v = inputs(length, seed=seed)
+    qg, kg, vg = _gpu(q, k, v)
+    idx, cnt = _random_lists(ref.num_blocks(length), seed)
+    backend = attention.AttentionBackend(register=False)
+    _, desc, tiles = backend._pool(kg, vg, False, True, True)
+    out, lse = backend._attention(qg, kg, tiles, torch.from_numpy(idx).cuda(),
+                                  torch.from_numpy(cnt).cuda(), SCALE, desc)
+    e_desc = ref.BlockDescriptors(*(to_np(getattr(desc, n)) for n in
+                                    ("mean_k", "mean_v", "var_k", "sigma_v", "counts")))
+    x_out, x_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE)
+    m_out, m_lse = ref.mean_tail(to_np(q), e_desc, ref.mask_from_indices(idx, cnt), SCALE)
+    e_out, e_lse = ref.merge_exact_mean(x_out, x_lse, m_out, m_lse)
+    # rows with no key at all (tile 0 with an empty list: no listed block, no tail)
+    # have LSE -inf; the oracle's merge gives NaN there, the kernel its empty-row 0
+    finite = np.isfinite(e_lse)
+    a_out, a_lse = to_np(out), to_np(lse)
+    assert_output_close(a_out[finite], e_out[finite], what="fused mean, random lists")
+    assert (a_out[~finite] == 0).all()
+    np.testing.assert_array_equal(np.isfinite(a_lse), finite)
+    np.testing.assert_allclose(a_lse[finite], e_lse[finite], atol=0.02, rtol=0.01)
