@@ -559,3 +559,31 @@ def test_sparse_attention_mean_random_lists(gpu, length, seed):
     assert (a_out[~finite] == 0).all()
     np.testing.assert_array_equal(np.isfinite(a_lse), finite)
     np.testing.assert_allclose(a_lse[finite], e_lse[finite], atol=0.02, rtol=0.01)
+
+
+@pytest.mark.parametrize("remainder", (False, True))
+def test_sparse_attention_rescue_random_lists(gpu, remainder):
+    """The fused rescue launch (exact blocks + one rescue token, and with remainder
+    the block's other tokens' mean, per unlisted causal block) on random unsorted
+    lists with repeats: against the oracle's exact part, rescue tail (the GPU's token
+    choice) and logaddexp merge (kernels.py:233-325)."""
+    length, seed = 1089, 113
+    q, k, v = inputs(length, seed=seed)
+    qg, kg, vg = _gpu(q, k, v)
+    idx, cnt = _random_lists(ref.num_blocks(length), seed)
+    backend = attention.AttentionBackend(register=False)
+    _, desc, tiles = backend._pool(kg, vg, False, remainder, True)
+    choice = kernels.rescue_choice(qg, tiles[0])
+    out, lse = backend._attention(qg, kg, tiles, torch.from_numpy(idx).cuda(),
+                                  torch.from_numpy(cnt).cuda(), SCALE, None,
+                                  rescue=(choice, remainder, desc, vg))
+    x_out, x_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE)
+    r_out, r_lse = ref.rescue_tail(to_np(q), to_np(k), to_np(v), ref.mask_from_indices(idx, cnt),
+                                   SCALE, remainder=remainder, choice=to_np(choice))
+    e_out, e_lse = ref.merge_exact_mean(x_out, x_lse, r_out, r_lse)
+    finite = np.isfinite(e_lse)   # -inf: tile 0 with an empty list (no key at all)
+    a_out, a_lse = to_np(out), to_np(lse)
+    assert_output_close(a_out[finite], e_out[finite], what="fused rescue, random lists")
+    assert (a_out[~finite] == 0).all()
+    np.testing.assert_array_equal(np.isfinite(a_lse), finite)
+    np.testing.assert_allclose(a_lse[finite], e_lse[finite], atol=0.02, rtol=0.01)
