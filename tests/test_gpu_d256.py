@@ -232,3 +232,44 @@ def test_unsupported_head_dim_raises(gpu):
         with pytest.raises(ValueError, match="head_dim"):
             backend.forward(_Layer(), q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
                             None, 64 ** -0.5)
+
+
+@pytest.mark.parametrize("tail", ("none", "mean", "rescue_v2"))
+def test_random_unsorted_lists(gpu, tail):
+    """The head_dim 256 kernel on seeded random lists (random subsets of the causal
+    blocks in random order, repeats, empty rows, garbage past the counts): exact
+    blocks alone, with the fused block-mean tail, and with the fused rescue tail and
+    remainder, against the oracle's exact part, tail and logaddexp merge."""
+    from tests.test_gpu_kernels import _random_lists
+    length, seed = 1089, 127
+    q, k, v = qkv(length, seed=seed)
+    qg, kg, vg = q.cuda(), k.cuda(), v.cuda()
+    idx, cnt = _random_lists(ref.num_blocks(length), seed, heads=Q_HEADS)
+    backend = attention.AttentionBackend(register=False)
+    _, desc, tiles = backend._pool(kg, vg, False, tail != "none", True)
+    ig, cg = torch.from_numpy(idx).cuda(), torch.from_numpy(cnt).cuda()
+    x_out, x_lse = ref.exact_attention(to_np(q), to_np(k), to_np(v), idx, cnt, SCALE,
+                                       precision="f32")
+    sel = ref.mask_from_indices(idx, cnt)
+    if tail == "none":
+        out, lse = backend._attention(qg, kg, tiles, ig, cg, SCALE, None)
+        e_out, e_lse = x_out, x_lse
+    elif tail == "mean":
+        out, lse = backend._attention(qg, kg, tiles, ig, cg, SCALE, desc)
+        e_desc = ref.BlockDescriptors(*(to_np(getattr(desc, n)) for n in
+                                        ("mean_k", "mean_v", "var_k", "sigma_v", "counts")))
+        m_out, m_lse = ref.mean_tail(to_np(q), e_desc, sel, SCALE)
+        e_out, e_lse = ref.merge_exact_mean(x_out, x_lse, m_out, m_lse)
+    else:
+        choice = kernels.rescue_choice(qg, tiles[0])
+        out, lse = backend._attention(qg, kg, tiles, ig, cg, SCALE, None,
+                                      rescue=(choice, True, desc, vg))
+        r_out, r_lse = ref.rescue_tail(to_np(q), to_np(k), to_np(v), sel, SCALE, remainder=True,
+                                       choice=to_np(choice))
+        e_out, e_lse = ref.merge_exact_mean(x_out, x_lse, r_out, r_lse)
+    finite = np.isfinite(e_lse)   # -inf: tile 0 with an empty list (no key at all)
+    a_out, a_lse = to_np(out), to_np(lse)
+    assert_output_close(a_out[finite], e_out[finite], what=f"d256 random lists, tail {tail}")
+    assert (a_out[~finite] == 0).all()
+    np.testing.assert_array_equal(np.isfinite(a_lse), finite)
+    np.testing.assert_allclose(a_lse[finite], e_lse[finite], atol=0.02, rtol=0.01)
