@@ -60,3 +60,37 @@ def test_methods_other_head_counts(gpu, heads, method):
     # peaky softmax: outputs reach several units, where one bf16 rounding step is 2^-5
     assert_output_close(to_np(out), expected["output"], what=f"{method} {q_heads}/{kv_heads}",
                         rel=2.0 ** -7)
+
+
+def _fuzz_cases(n=16, seed=2024):
+    """Deterministic random layer shapes: batch, length (partial last blocks, lone
+    tiles), head layout, method and alpha."""
+    rng = np.random.default_rng(seed)
+    layouts = ((4, 1), (6, 3), (8, 2), (12, 4), (28, 4), (16, 16))
+    cases = []
+    for i in range(n):
+        cases.append((int(rng.integers(1, 4)), int(rng.integers(1, 900)),
+                      layouts[int(rng.integers(len(layouts)))],
+                      attention.METHODS[int(rng.integers(len(attention.METHODS)))],
+                      float(rng.choice((0.08, 0.5, 0.7))), 1000 + i))
+    return cases
+
+
+@pytest.mark.parametrize("batch,length,heads,method,alpha,seed", _fuzz_cases())
+def test_random_layer_shapes(gpu, batch, length, heads, method, alpha, seed):
+    """Seeded random shapes through the backend against the oracle layer (Q, K x 4 so
+    that routing drops blocks)."""
+    q_heads, kv_heads = heads
+    q, k, v, _ = synthetic.make_inputs(length, seed=seed, q_heads=q_heads, kv_heads=kv_heads,
+                                       batch=batch)
+    q = (q.float() * 4.0).to(torch.bfloat16)
+    k = (k.float() * 4.0).to(torch.bfloat16)
+    backend = attention.AttentionBackend(alpha=alpha, register=False)
+    backend.configure(method, alpha)
+    out, _ = backend.forward(_Layer(), q.cuda().transpose(1, 2), k.cuda().transpose(1, 2),
+                             v.cuda().transpose(1, 2), None, SCALE)
+    expected = ref.attention_layer(to_np(q), to_np(k), to_np(v), SCALE, method, alpha)
+    assert out.shape == (batch, length, q_heads, 128)
+    assert_output_close(to_np(out), expected["output"],
+                        what=f"{method} b{batch} S{length} {q_heads}/{kv_heads} a{alpha}",
+                        rel=2.0 ** -7)
