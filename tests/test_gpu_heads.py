@@ -8,7 +8,8 @@ Q and K are scaled by 4 and alpha is 0.7 so that routing drops blocks: with
 unscaled random inputs the block-mean proxy is nearly flat and the sink,
 window and last-tile protection at 17 blocks keeps every causal block, which
 would leave the sparse lists and the mean / rescue tails of these head layouts
-untested."""
+untested. Also seeded random layer shapes (batch, length, head layout, method,
+alpha) against the oracle layer."""
 
 import numpy as np
 import pytest
