@@ -495,6 +495,49 @@ def test_selection_accounting(gpu):
             assert got == value, key
 
 
+def _selection_params(n=12, seed=31):
+    """Deterministic random selection parameters: sink, window and last-full block
+    counts (0 included), alpha (0 included), the top-k budget of deal_output_score,
+    the score layout."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        out.append((int(rng.integers(1, 3)), int(rng.choice((9, 37, 64, 65, 130))),
+                    int(rng.integers(1, 6)), int(rng.integers(0, 4)), int(rng.integers(0, 7)),
+                    int(rng.integers(0, 4)), float(rng.choice((0.0, 0.05, 0.3, 0.9, 1.0))),
+                    int(rng.choice((0, 0, 3, 10))), 500 + i))
+    return out
+
+
+@pytest.mark.parametrize("batch,blocks,heads,sink,window,last,alpha,budget,seed",
+                         _selection_params())
+def test_selection_random_parameters_bit_exact(gpu, batch, blocks, heads, sink, window, last,
+                                               alpha, budget, seed):
+    """protected_selection (mask, indices, counts) and deal_output_score (its top-k
+    budget included) over random sink / window / last-block counts, alphas and score
+    layouts, with zero rows, repeated maxima and exact threshold ties planted: bit for
+    bit against the oracle (kernels.py:129-160, upstream:357-407)."""
+    rng = np.random.default_rng(seed)
+    scores = rng.random((batch, blocks, blocks, heads), dtype=np.float32) ** 3
+    scores[:, min(4, blocks - 1)] = 0.0                          # a zero row
+    scores[:, :, 0, :] = scores.max()                            # repeated maxima
+    tie = rng.integers(0, blocks, size=3)
+    scores[:, :, tie, :] = np.float32(alpha) * scores.max()      # threshold ties
+    sg = torch.from_numpy(scores).cuda()
+    indices = torch.empty(scores.shape, dtype=torch.int64, device="cuda")
+    counts = torch.empty(scores.shape[:2] + scores.shape[3:], dtype=torch.int32, device="cuda")
+    mask = kernels.protected_selection(sg, alpha, sink, window, last, indices, counts)
+    expected = ref.protected_selection(scores, alpha, sink, window, last)
+    np.testing.assert_array_equal(to_np(mask), expected)
+    e_idx, e_cnt = ref.indices_from_mask(expected)
+    np.testing.assert_array_equal(to_np(counts), e_cnt)
+    np.testing.assert_array_equal(to_np(indices), e_idx)
+    idx, cnt = up.deal_output_score(sg, sink, window, alpha, last, budget)
+    e_idx, e_cnt = ref.deal_output_score(scores, sink, window, alpha, last, budget)
+    np.testing.assert_array_equal(to_np(cnt), e_cnt)
+    np.testing.assert_array_equal(to_np(idx), e_idx)
+
+
 def _random_lists(blocks, seed, heads=28):
     """For every (tile, head) a random subset of the causal blocks 0..t in random
     order, some entries repeated, a random count (empty rows included), and garbage
