@@ -128,6 +128,32 @@ def test_v1_route_non_positive_scale(gpu, scale):
     np.testing.assert_array_equal(to_np(cnt), e_cnt)
 
 
+@pytest.mark.parametrize("sink,window,last,alpha", [(0, 0, 0, 0.3), (1, 6, 3, 0.9), (3, 1, 0, 0.05),
+                                                   (0, 2, 1, 1.0), (2, 4, 2, 0.0), (5, 9, 4, 0.5)])
+def test_v1_route_protection_parameters(gpu, sink, window, last, alpha):
+    """The fused route with the backend's sink / window / last-block settings away
+    from the defaults (0 included) and alphas 0 to 1: its mask equals the selection
+    rule on its own scores, its lists and counts that mask's, and the scores match
+    the oracle's."""
+    length = 4096 - 70    # 32 blocks, the last one partial
+    q, k, v = inputs(length, seed=17 + sink + 3 * window)
+    q = (q.float() * 3).to(torch.bfloat16)
+    qg, kg, vg = _gpu(q, k, v)
+    backend = attention.AttentionBackend(alpha=alpha, sink_blocks=sink, window_blocks=window,
+                                         last_full_blocks=last, register=False)
+    backend.configure("fp_v1", alpha)
+    record = {"events": {}}
+    _, kbar, scores, idx, cnt, sel = backend._v1_selection(qg, kg, SCALE, record, vg, True)
+    g_scores = to_np(scores)
+    np.testing.assert_allclose(g_scores, ref.v1_scores(to_np(q), to_np(kbar), SCALE),
+                               atol=2e-4, rtol=0.005)
+    own = ref.mask_from_indices(*ref.deal_output_score(g_scores, sink, window, alpha, last, 0))
+    np.testing.assert_array_equal(to_np(sel), own)
+    e_idx, e_cnt = ref.indices_from_mask(own)
+    np.testing.assert_array_equal(to_np(cnt), e_cnt)
+    np.testing.assert_array_equal(to_np(idx), e_idx)
+
+
 def test_v1_route_head_groups(gpu):
     """The routed form writes each tile's [NB, Hq] index and mask slabs from LDS
     lists, in passes over groups of heads when Hq x NB exceeds its 32768-entry
