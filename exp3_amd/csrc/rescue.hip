@@ -80,6 +80,7 @@ struct ChoiceArgs {
   const uint16_t* kt;    // key tiles [B, Hkv, NB, 128, D] (swizzled)
   uint8_t* choice;       // [B, NB, NB, Hq]
   int batch, q_heads, kv_heads, blocks, group;
+  int splits;            // workgroups sharing one (key block, kv group)'s columns
 };
 
 __device__ __forceinline__ bf16x8 pack_bf16x8(const float (&x)[8]) {
@@ -89,7 +90,11 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(const float (&x)[8]) {
   return as_bf16x8(r);
 }
 
-// One workgroup per (key block j, kv group g, batch b). The key tile of block j
+// Workgroups (key block j, kv group g, split s, batch b): the (later tile, q head)
+// columns of block j are dealt in 32-column groups over the splits workgroups of
+// (j, g) and their four waves (group s * 4 + w, then every splits * 4-th), so the
+// early key blocks, which have the most later tiles, are spread over as many
+// workgroups as the latest ones need. The key tile of block j
 // (pool layout: row = token, 16-byte chunk c of row r at c ^ (r & 15) for c < 16;
 // at D = 256, chunk c < 32 at (c & 16) | ((c & 15) ^ (r & 15))) is staged in LDS once; its 128 token rows are the MFMA A operand (four 32-row tiles). The
 // columns are the (later tile t, q head) pairs of the group, 32 per wave step; their
@@ -98,20 +103,26 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(const float (&x)[8]) {
 // Each lane then owns one column's 128 token scores (64 per lane half, in token
 // order): a strict in-lane max keeps the first position, and the two halves merge
 // with the lower position on equal scores (torch.argmax: first maximum).
+// Four waves per SIMD at D = 128 (at most 128 registers each); at D = 256 the 64 KB
+// key tile allows two workgroups per CU.
 template <int D>
-__global__ __launch_bounds__(kChoiceThreads) void rescue_choice_kernel(ChoiceArgs a) {
+__global__ __launch_bounds__(kChoiceThreads, D == 128 ? 4 : 2) void rescue_choice_kernel(ChoiceArgs a) {
   const int j = blockIdx.x;
-  const int g = blockIdx.y;
+  const int g = blockIdx.y / a.splits, split = blockIdx.y % a.splits;
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
-  // entries of tiles t <= j (no rescue token) are written as 0
-  for (int i = tid; i < (j + 1) * a.group; i += kChoiceThreads) {
-    const int t = i / a.group, hh = i % a.group;
-    a.choice[(((int64_t)b * a.blocks + t) * a.blocks + j) * a.q_heads + g * a.group + hh] = 0;
+  // entries of tiles t <= j (no rescue token) are written as 0, by split 0
+  if (split == 0) {
+    for (int i = tid; i < (j + 1) * a.group; i += kChoiceThreads) {
+      const int t = i / a.group, hh = i % a.group;
+      a.choice[(((int64_t)b * a.blocks + t) * a.blocks + j) * a.q_heads + g * a.group + hh] = 0;
+    }
   }
-  if (j >= a.blocks - 1) return;  // no later tile
+  const int ncols = a.group * (a.blocks - 1 - j);   // 0 for the last block
+  const int ngroups = (ncols + 31) / 32;
+  if (split * (kChoiceThreads / 64) >= ngroups) return;   // no column group here
 
   __shared__ __align__(16) uint16_t kt[kBlock * D];  // 32 KB (64 KB at D = 256)
   {
@@ -122,12 +133,11 @@ __global__ __launch_bounds__(kChoiceThreads) void rescue_choice_kernel(ChoiceArg
   }
   block_sync();
 
-  const int ncols = a.group * (a.blocks - 1 - j);
-  const int ngroups = (ncols + 31) / 32;
   // LDS element offset of token row (32 rt + col), chunk 2 dc + half:
   // (dc >> 3) * 128 + (base ^ ((dc & 7) << 4)), plus rt * 32 rows
   const int e0 = (((col >> 1) & 7) << 4) + ((half ^ (col & 1)) << 3);
-  for (int grp = w; grp < ngroups; grp += kChoiceThreads / 64) {
+  for (int grp = split * (kChoiceThreads / 64) + w; grp < ngroups;
+       grp += a.splits * (kChoiceThreads / 64)) {
     const int c = grp * 32 + col;
     const bool cok = c < ncols;
     const int t = j + 1 + (cok ? c / a.group : 0);
@@ -135,7 +145,10 @@ __global__ __launch_bounds__(kChoiceThreads) void rescue_choice_kernel(ChoiceArg
     const float* qm = a.qmean + (((int64_t)b * a.blocks + t) * a.q_heads + g * a.group + hh) * D +
                       half * 8;
     f32x16 acc[4] = {};
-#pragma unroll
+    // four k-steps per iteration: their mean-query loads and splits are formed
+    // shortly before their products instead of all being hoisted (which held 192
+    // registers and allowed two waves per SIMD)
+#pragma unroll 4
     for (int dc = 0; dc < D / 16; ++dc) {
       float x[8] = {};
       if (cok) {
@@ -232,8 +245,14 @@ extern "C" int spx_rescue_choice(const float* qmean, const void* key_tiles, int 
   a.choice = choice;
   a.batch = batch; a.q_heads = q_heads; a.kv_heads = kv_heads; a.blocks = num_blocks(seq);
   a.group = q_heads / kv_heads;
+  // enough splits that the first key block's column groups come to about four per wave
+  // (two per wave ran the same at d = 128 and 8 % slower at d = 256, where every
+  // workgroup stages a 64 KB key tile)
+  const int max_groups = (a.group * (a.blocks - 1) + 31) / 32;
+  a.splits = std::max(1, std::min(16, (max_groups + 4 * (kChoiceThreads / 64) - 1) /
+                                          (4 * (kChoiceThreads / 64))));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  dim3 grid(a.blocks, kv_heads, batch);
+  dim3 grid(a.blocks, kv_heads * a.splits, batch);
   if (head_dim == 256) rescue_choice_kernel<256><<<grid, kChoiceThreads, 0, st>>>(a);
   else rescue_choice_kernel<kHeadDim><<<grid, kChoiceThreads, 0, st>>>(a);
   return launch_status("rescue_choice");
